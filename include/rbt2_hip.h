@@ -1,0 +1,128 @@
+/*
+ * rbt2_hip.h -- C ABI of the MI355X (gfx950) MoE-layer path for the RABBIT2 engine.
+ *
+ * The reference engine (rabbit2/src/rabbit2.c) is one C99 file whose MoE feed-forward block
+ * (:511-542) runs on three static seams: matvec() (:357), get_expert() (:261) and forward()
+ * (:455). This header is the boundary that replaces them: plain C types, plain pointers and sizes,
+ * int 1 = ok / 0 = error (the engine's convention, e.g. load_model :199, forward :455), with the
+ * message kept per handle (rbt_hip_last_error) and also printed to stderr like the engine does.
+ *
+ * Threading: a handle is used by one host thread at a time (the engine is single-threaded,
+ * rabbit2/README.md:255). All device work of a handle runs in order on the handle's own HIP
+ * stream. Calls ending in _dev take device pointers and are asynchronous on that stream; every
+ * other call takes host pointers and returns when its results are in host memory.
+ */
+#ifndef RBT2_HIP_H
+#define RBT2_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RBT_DT_F32 0  /* rabbit2.c:60 */
+#define RBT_DT_BF16 1 /* rabbit2.c:61 */
+
+/* Which CPU summation order the router logits reproduce bit for bit, so that expert selection is
+ * identical to the engine's (top-k over softmax probabilities, strict '>', lowest index wins):
+ *   RBT_ORDER_SCALAR  rabbit2.c:356-390 (--kernel scalar, and the engine's default)
+ *   RBT_ORDER_AVX2    rabbit2.c:323-353 (--kernel auto|avx2 on AVX2 hosts) -- the default here */
+#define RBT_ORDER_SCALAR 0
+#define RBT_ORDER_AVX2 1
+
+typedef struct rbt_hip rbt_hip; /* opaque: one device, one stream, owns its device memory */
+
+/* Bytes 8..67 of a .rbt2 file header; same field order as Config (rabbit2.c:63-69). */
+typedef struct {
+    int32_t vocab, dim, n_layers, n_heads, n_kv_heads, head_dim;
+    int32_t n_experts, top_k, expert_hidden, max_seq;
+    int32_t dtype, qk_norm, norm_topk;
+    float rope_theta, rms_eps;
+} rbt_config;
+
+/* One MoE layer in device memory, in the .rbt2 storage format (rabbit2.c:173, :186-189):
+ * router [n_experts][dim] in dtype; expert e's blob at experts + e*expert_stride holding
+ * w1[H][D] | w3[H][D] | w2[D][H] (w1 = gate, w3 = up, w2 = down), row-major, dtype elements.
+ * router_bias: optional device [n_experts] f32 added to the router logits before the softmax
+ * (no counterpart in the reference; used to build skewed-routing workloads), else NULL. */
+typedef struct {
+    int32_t dim, n_experts, top_k, expert_hidden, dtype, norm_topk;
+    const void *router;
+    const void *experts;
+    uint64_t expert_stride;
+    const float *router_bias;
+} rbt_moe_layer;
+
+/* ---- lifetime (replaces the engine's Model/State setup, rabbit2.c:199-228, :427-451) ---- */
+int rbt_hip_init(rbt_hip **out, int device);
+void rbt_hip_free(rbt_hip *h);
+/* Last error message of this handle ("" if none); with h == NULL, the last init failure. */
+const char *rbt_hip_last_error(const rbt_hip *h);
+int rbt_hip_set_router_order(rbt_hip *h, int order);
+
+/* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the
+ * header exactly like load_model() (rabbit2.c:199-228) and keeps every expert resident, which
+ * replaces the engine's get_expert() streaming and LRU cache (rabbit2.c:233-300): 16 x 64 OLMoE
+ * experts are 12 GiB of the 288 GB HBM. Fills *cfg (may be NULL). */
+int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config *cfg);
+/* Device view of layer `layer` of the uploaded model (for the _dev calls). */
+int rbt_hip_layer(rbt_hip *h, int layer, rbt_moe_layer *out);
+
+/* ---- the MoE block (replaces rabbit2.c:513-542; the rmsnorm at :512 stays with the caller) ----
+ * xb [T][dim] normalised input. x_inout [T][dim] receives x += moe (may be NULL).
+ * routing_out [T][top_k] the chosen experts in selection order (the --dump routing record,
+ * rabbit2.c:527), may be NULL. T may be 0. Host pointers; synchronous. */
+int rbt_hip_moe(rbt_hip *h, int layer, const float *xb, int T, float *x_inout, int32_t *routing_out);
+
+/* Same block on device pointers, asynchronous on the handle stream. Any output may be NULL:
+ *   x_dev       [T][dim]    x += moe
+ *   moe_dev     [T][dim]    the block output itself
+ *   routing_dev [T][top_k]  int32 expert ids, selection order
+ *   weights_dev [T][top_k]  combine weights (after norm_topk renormalisation, rabbit2.c:539)
+ * Workspace is taken from the handle; it grows (hipMalloc) only when T exceeds every earlier
+ * call's T, so call rbt_hip_reserve() first to keep allocation off the per-token path. */
+int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, float *x_dev, float *moe_dev,
+                    int32_t *routing_dev, float *weights_dev);
+int rbt_hip_reserve(rbt_hip *h, const rbt_moe_layer *L, int max_tokens);
+
+/* Tokens-per-expert histogram of the last rbt_hip_moe_dev call that used the grouped (prefill)
+ * path, [n_experts] int32, device pointer owned by the handle; NULL if none. */
+const int32_t *rbt_hip_expert_counts_dev(rbt_hip *h);
+
+/* ---- the dense seam (replaces matvec(), rabbit2.c:357, for weights of the uploaded model) ----
+ * out[r] = dot(W[r,:], x), W at byte offset w_offset of the uploaded image, [rows][cols] in the
+ * model dtype. Host pointers; synchronous. */
+int rbt_hip_matvec(rbt_hip *h, float *out, uint64_t w_offset, const float *x, int rows, int cols);
+int rbt_hip_matvec_dev(rbt_hip *h, float *out_dev, const void *W_dev, int dtype, const float *x_dev, int rows,
+                       int cols);
+
+/* ---- device memory and stream plumbing for hosts without their own HIP code ---- */
+int rbt_hip_malloc(rbt_hip *h, void **dev, uint64_t bytes);
+int rbt_hip_free_dev(rbt_hip *h, void *dev);
+int rbt_hip_h2d(rbt_hip *h, void *dst_dev, const void *src, uint64_t bytes);
+int rbt_hip_d2h(rbt_hip *h, void *dst, const void *src_dev, uint64_t bytes);
+int rbt_hip_memset_dev(rbt_hip *h, void *dst_dev, int value, uint64_t bytes);
+int rbt_hip_synchronize(rbt_hip *h);
+void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work runs on */
+
+/* ---- instrumentation (the reference's only timing is its stderr tok/s line, rabbit2.c:742-744) ----
+ * While enabled, every kernel launch of rbt_hip_moe_dev is bracketed by HIP events on the handle
+ * stream and its duration is accumulated under its name ("router", "gateup", "down_combine",
+ * ...); each call then waits for its own work. rbt_hip_profile_get returns 0 for an unknown
+ * name. Meant for measurement passes, not for the timed hot loop. */
+int rbt_hip_profile_enable(rbt_hip *h, int on);
+int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches);
+
+/* Synthetic data (no counterpart in the reference, whose random weights come from NumPy,
+ * rabbit2/ref/reference.py:20-50): dst[i] = offset + scale * N(0,1) sample (first + i) of stream
+ * `stream` under `seed`, rounded to f32 then to dtype (bf16 round-to-nearest-even). The sample
+ * definition is SplitMix64 + Box-Muller, documented with the CPU twin in oracle/rbt2_oracle.h. */
+int rbt_hip_fill_normal(rbt_hip *h, void *dst_dev, int dtype, uint64_t n, uint64_t seed, uint64_t stream,
+                        uint64_t first, float scale, float offset);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

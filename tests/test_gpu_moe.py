@@ -1,0 +1,114 @@
+"""Parity of the HIP MoE layer (rbt_hip_moe_dev through the C ABI) with the oracle.
+
+Shapes follow the reference's engine tests (rabbit2/tests/test_forward.py:80-98 and
+rabbit2/tests/test_avx2.py:52: odd dims, tails below 16 columns, top-1, top-k of few experts,
+f32 and bf16) plus the OLMoE layer (D 2048, E 64, top-8, H 1024, bf16) at decode and prefill sizes.
+Bar: routing identical except at exact CPU ties; normwise max error <= 1e-3 (tests/common.py).
+"""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+from tests.common import MOE_RTOL, SynthLayer, normwise_err, routing_check
+
+pytestmark = pytest.mark.gpu
+
+ORDERS = [po.ORDER_AVX2, po.ORDER_SCALAR]
+
+
+def check(layer, xb, order, dev, x=None, label=""):
+    dev.set_router_order(order)
+    want = layer.oracle(xb, order, x=x)
+    got = layer.run_gpu(xb, x=x)
+    bad, unexplained = routing_check(got["routing"], want["routing"], want["probs"])
+    err = normwise_err(got["moe"], want["moe"])
+    werr = normwise_err(got["weights"], want["weights"])
+    print(f"{label} T={xb.shape[0]} order={order}: routing mismatched tokens {bad} (unexplained {unexplained}), "
+          f"moe err {err:.2e}, weight err {werr:.2e}", flush=True)
+    assert unexplained == 0
+    assert err <= MOE_RTOL
+    if bad == 0:
+        assert werr <= 1e-6
+    if x is not None:
+        assert normwise_err(got["x"], want["x"]) <= MOE_RTOL
+    return got, want
+
+
+SMALL_SHAPES = [
+    # (dim, E, K, H, dtype, norm_topk)
+    (64, 8, 2, 128, po.DT_F32, 1),     # reference Config() defaults
+    (64, 8, 2, 128, po.DT_BF16, 1),
+    (48, 6, 3, 40, po.DT_BF16, 0),     # OLMoE-like top-3 of 6
+    (36, 5, 2, 25, po.DT_F32, 1),      # odd dims
+    (32, 4, 1, 64, po.DT_F32, 1),      # top-1
+    (8, 4, 2, 7, po.DT_BF16, 0),       # dim < 16: whole row is the AVX2 tail
+    (36, 4, 2, 25, po.DT_BF16, 0),
+    (256, 8, 2, 128, po.DT_F32, 0),    # the tiny OLMoE-style model's MoE layer
+    (100, 7, 7, 33, po.DT_BF16, 1),    # K == E
+]
+
+
+@pytest.mark.parametrize("shape", SMALL_SHAPES, ids=[f"D{s[0]}E{s[1]}K{s[2]}H{s[3]}dt{s[4]}n{s[5]}" for s in SMALL_SHAPES])
+@pytest.mark.parametrize("order", ORDERS)
+def test_small_shapes(dev, shape, order):
+    D, E, K, H, dt, nt = shape
+    layer = SynthLayer(dev, D, E, K, H, dt, nt, seed=3, w_scale=1.0, fan_in=True)
+    try:
+        for T in (1, 5):
+            xb = layer.make_x(T, seed=11 + T, bf16=False)
+            x = layer.make_x(T, seed=99, bf16=False)
+            check(layer, xb, order, dev, x=x, label=f"D{D}E{E}K{K}H{H}")
+    finally:
+        layer.close()
+
+
+def test_empty_batch(dev):
+    layer = SynthLayer(dev, 64, 8, 2, 128, po.DT_BF16, 1, seed=1)
+    try:
+        got = layer.run_gpu(np.zeros((0, 64), np.float32))
+        assert got["moe"].shape == (0, 64)
+    finally:
+        layer.close()
+
+
+@pytest.fixture(scope="module")
+def olmoe_layer(dev):
+    """The OLMoE-1B-7B layer shape, bf16 weights ~N(0, 0.02), seed 1, renormalised top-8."""
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=1)
+    yield layer
+    layer.close()
+
+
+@pytest.mark.parametrize("order", ORDERS)
+def test_olmoe_decode(dev, olmoe_layer, order):
+    for s in range(4):
+        xb = olmoe_layer.make_x(1, seed=s)
+        check(olmoe_layer, xb, order, dev, label=f"olmoe decode seed {s}")
+
+
+def test_olmoe_decode_deterministic(dev, olmoe_layer):
+    dev.set_router_order(po.ORDER_AVX2)
+    xb = olmoe_layer.make_x(1, seed=7)
+    a = olmoe_layer.run_gpu(xb)
+    b = olmoe_layer.run_gpu(xb)
+    assert a["moe"].tobytes() == b["moe"].tobytes()
+    assert np.array_equal(a["routing"], b["routing"])
+
+
+@pytest.mark.parametrize("biased", [False, True], ids=["uniform", "skewed"])
+def test_olmoe_prefill(dev, biased):
+    """512 tokens; skewed: +2.0 on the router logits of experts 0-7 (CPU and GPU alike)."""
+    bias = np.zeros(64, np.float32)
+    if biased:
+        bias[:8] = 2.0
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=1, bias=bias)
+    try:
+        xb = layer.make_x(512, seed=5)
+        got, want = check(layer, xb, po.ORDER_AVX2, dev, label="olmoe prefill " + ("skewed" if biased else "uniform"))
+        hist = np.bincount(want["routing"].ravel(), minlength=64)
+        print("tokens per expert:", hist.tolist(), flush=True)
+        assert hist.sum() == 512 * 8
+        if biased:
+            assert hist[:8].sum() > hist[8:].sum()
+    finally:
+        layer.close()
