@@ -84,6 +84,9 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch every layer from Python instead of replaying a "
                     "captured HIP graph of the steps")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target length of the CPU baseline sample")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this size (a known-size kernel for scaling "
+                         "FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -180,7 +183,7 @@ def main():
     for s in range(nprof):
         step(s)
     kern = {}
-    for name in ("router", "gateup", "down_combine"):
+    for name in ("router", "topk", "gateup", "down_combine"):
         tot, n = dev.profile_get(name)
         kern[name] = {"avg_us": 1000.0 * tot / max(n, 1), "launches": n}
     dev.profile(False)
@@ -189,17 +192,39 @@ def main():
     gateup_bytes = w_gateup + D * 4 + K * H * 4  # weights + x read + h written
     down_bytes = K * D * H * esz + K * H * 4 + D * 4
     router_bytes = E * D * esz + D * 4
+    topk_bytes = E * 4 * 2 + K * 8  # logits in, probabilities out, routing + weights out
     layer_alg = E * D * esz + K * 3 * H * D * esz  # 100,925,440: router + 8 experts
-    for name, b in (("router", router_bytes), ("gateup", gateup_bytes), ("down_combine", down_bytes)):
+    for name, b in (("router", router_bytes), ("topk", topk_bytes), ("gateup", gateup_bytes),
+                    ("down_combine", down_bytes)):
         kern[name]["alg_bytes"] = b
         kern[name]["GBps"] = b / (kern[name]["avg_us"] * 1e-6) / 1e9
     dom = kern["gateup"]
     layer_us = 1000.0 * ms_per_step / LAYERS
     layer_gbs = layer_alg / (layer_us * 1e-6) / 1e9
 
+    if args.copy_calib_mib:
+        nb = args.copy_calib_mib << 20
+        src, dst = dev.malloc(nb), dev.malloc(nb)
+        dev.memset(src, 1)
+        hipapi.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        assert hipapi.hipMemcpyAsync(dst.p, src.p, nb, 3, stream) == 0  # hipMemcpyDeviceToDevice
+        dev.synchronize()
+        dev.free(src)
+        dev.free(dst)
+
     # routing histogram sanity (the last step's selections)
     last_routing = dev.d2h(routing, (LAYERS, K), np.int32)
     assert np.all((last_routing >= 0) & (last_routing < E))
+
+    # HBM bytes per launch of the dominant kernel, from the calibrated rocprofv3 --pmc runs kept
+    # under profiles/ (counters cannot be read from inside this process)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "olmoe_moe_decode_bs1_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath))["per_launch"]["gateup_fast"]["bytes"]
+        except (KeyError, ValueError):
+            traffic = None
 
     value = 1000.0 / ms_per_step
     out = {
@@ -230,7 +255,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": "profiles/olmoe_moe_decode_bs1_traffic.json" if traffic else None,
             "alg_bytes_per_launch": gateup_bytes,
             "avg_launch_us": round(dom["avg_us"], 3),
         },

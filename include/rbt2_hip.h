@@ -109,8 +109,8 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
 
 /* ---- instrumentation (the reference's only timing is its stderr tok/s line, rabbit2.c:742-744) ----
  * While enabled, every kernel launch of rbt_hip_moe_dev is bracketed by HIP events on the handle
- * stream and its duration is accumulated under its name ("router", "gateup", "down_combine",
- * ...); each call then waits for its own work. rbt_hip_profile_get returns 0 for an unknown
+ * stream and its duration is accumulated under its name ("router", "topk", "gateup",
+ * "down_combine"); each call then waits for its own work. rbt_hip_profile_get returns 0 for an unknown
  * name. Meant for measurement passes, not for the timed hot loop. */
 int rbt_hip_profile_enable(rbt_hip *h, int on);
 int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches);

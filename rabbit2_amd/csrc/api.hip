@@ -25,8 +25,8 @@ struct LayerOff {
     uint64_t attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, router, experts;
 };
 
-enum ProfKernel { kProfRouter, kProfGateup, kProfDown, kProfCount };
-const char *const kProfNames[kProfCount] = {"router", "gateup", "down_combine"};
+enum ProfKernel { kProfRouter, kProfTopk, kProfGateup, kProfDown, kProfCount };
+const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_combine"};
 
 struct Profile {
     bool on = false;
@@ -39,7 +39,6 @@ struct Profile {
 struct Workspace {
     int tokens = 0, E = 0, K = 0, H = 0;
     float *probs = nullptr;       // [T][E]
-    unsigned *counters = nullptr; // [T], zero between launches
     int32_t *routing = nullptr;   // [T][K]
     float *weights = nullptr;     // [T][K]
     float *hbuf = nullptr;        // [T*K][H]
@@ -149,7 +148,6 @@ int check_layer(rbt_hip *h, const rbt_moe_layer *L) {
 
 void ws_release(Workspace &w) {
     (void)hipFree(w.probs);
-    (void)hipFree(w.counters);
     (void)hipFree(w.routing);
     (void)hipFree(w.weights);
     (void)hipFree(w.hbuf);
@@ -165,11 +163,9 @@ int ws_reserve(rbt_hip *h, int T, int E, int K, int H) {
     HIP_OK(h, hipStreamSynchronize(h->stream));
     ws_release(w);
     HIP_OK(h, hipMalloc(&w.probs, sizeof(float) * (size_t)nT * nE));
-    HIP_OK(h, hipMalloc(&w.counters, sizeof(unsigned) * (size_t)nT));
     HIP_OK(h, hipMalloc(&w.routing, sizeof(int32_t) * (size_t)nT * nK));
     HIP_OK(h, hipMalloc(&w.weights, sizeof(float) * (size_t)nT * nK));
     HIP_OK(h, hipMalloc(&w.hbuf, sizeof(float) * (size_t)nT * nK * nH));
-    HIP_OK(h, hipMemsetAsync(w.counters, 0, sizeof(unsigned) * (size_t)nT, h->stream));
     w.tokens = nT;
     w.E = nE;
     w.K = nK;
@@ -188,17 +184,17 @@ int stage_reserve(rbt_hip *h, uint64_t bytes) {
     return 1;
 }
 
-int prof_begin(rbt_hip *h, int k) {
-    if (!h->prof.on) return 1;
-    HIP_OK(h, hipEventRecord(h->prof.ev[k][0], h->stream));
-    return 1;
-}
-
-int prof_end(rbt_hip *h, int k) {
-    if (!h->prof.on) return 1;
-    HIP_OK(h, hipEventRecord(h->prof.ev[k][1], h->stream));
-    h->prof.used[k] = true;
-    return 1;
+// The launch context of kernel k: the handle stream, plus (when profiling) the event pair that
+// hipExtLaunchKernel stamps with that kernel's own start and end.
+Launch lc(rbt_hip *h, int k) {
+    Launch L;
+    L.s = h->stream;
+    if (h->prof.on && k >= 0) {
+        L.start = h->prof.ev[k][0];
+        L.stop = h->prof.ev[k][1];
+        h->prof.used[k] = true;
+    }
+    return L;
 }
 
 // Waits for the call's events and adds each bracketed kernel's duration.
@@ -332,16 +328,20 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
     Workspace &w = h->ws;
     int32_t *routing = routing_dev ? routing_dev : w.routing;
     float *weights = weights_dev ? weights_dev : w.weights;
-    if (!prof_begin(h, kProfRouter)) return 0;
-    HIP_OK(h, launch_router(h->stream, h->order, L->dtype, xb_dev, L->router, L->router_bias, T, L->n_experts, L->dim,
-                            L->top_k, L->norm_topk, w.probs, w.counters, routing, weights));
-    if (!prof_end(h, kProfRouter) || !prof_begin(h, kProfGateup)) return 0;
-    HIP_OK(h, launch_gateup_gemv(h->stream, L->dtype, L->experts, L->expert_stride, routing, xb_dev, T, L->top_k,
-                                 L->dim, L->expert_hidden, w.hbuf));
-    if (!prof_end(h, kProfGateup) || !prof_begin(h, kProfDown)) return 0;
-    HIP_OK(h, launch_down_combine(h->stream, L->dtype, L->experts, L->expert_stride, routing, weights, w.hbuf, T,
-                                  L->top_k, L->dim, L->expert_hidden, x_dev, moe_dev));
-    if (!prof_end(h, kProfDown)) return 0;
+    HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
+                            L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
+                            weights));
+    if (experts_decode_supported(L->dtype, T, L->top_k, L->dim, L->expert_hidden, L->experts, L->expert_stride, xb_dev,
+                                 w.hbuf)) {
+        HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
+                                        routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
+                                        moe_dev));
+    } else {
+        HIP_OK(h, launch_gateup_gemv(lc(h, kProfGateup), L->dtype, L->experts, L->expert_stride, routing, xb_dev, T,
+                                     L->top_k, L->dim, L->expert_hidden, w.hbuf));
+        HIP_OK(h, launch_down_combine(lc(h, kProfDown), L->dtype, L->experts, L->expert_stride, routing, weights,
+                                      w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev, moe_dev));
+    }
     return prof_collect(h);
 }
 
@@ -381,7 +381,7 @@ int rbt_hip_matvec_dev(rbt_hip *h, float *out_dev, const void *W_dev, int dtype,
     if (rows == 0) return 1;
     if (!out_dev || !W_dev || !x_dev) return fail(h, "matvec: NULL pointer");
     if (!set_device(h)) return 0;
-    HIP_OK(h, launch_matvec(h->stream, dtype, W_dev, x_dev, out_dev, rows, cols));
+    HIP_OK(h, launch_matvec(lc(h, -1), dtype, W_dev, x_dev, out_dev, rows, cols));
     return 1;
 }
 
@@ -400,7 +400,7 @@ int rbt_hip_matvec(rbt_hip *h, float *out, uint64_t w_offset, const float *x, in
     uint8_t *st = static_cast<uint8_t *>(h->stage);
     float *x_d = reinterpret_cast<float *>(st), *o_d = reinterpret_cast<float *>(st + o_off);
     HIP_OK(h, hipMemcpyAsync(x_d, x, (uint64_t)cols * 4, hipMemcpyHostToDevice, h->stream));
-    HIP_OK(h, launch_matvec(h->stream, h->cfg.dtype, h->model + w_offset, x_d, o_d, rows, cols));
+    HIP_OK(h, launch_matvec(lc(h, -1), h->cfg.dtype, h->model + w_offset, x_d, o_d, rows, cols));
     HIP_OK(h, hipMemcpyAsync(out, o_d, (uint64_t)rows * 4, hipMemcpyDeviceToHost, h->stream));
     HIP_OK(h, hipStreamSynchronize(h->stream));
     return 1;
@@ -498,7 +498,7 @@ int rbt_hip_fill_normal(rbt_hip *h, void *dst_dev, int dtype, uint64_t n, uint64
     if (!n) return 1;
     if (!dst_dev) return fail(h, "fill_normal: NULL pointer");
     if (!set_device(h)) return 0;
-    HIP_OK(h, launch_fill_normal(h->stream, dst_dev, dtype, n, seed, stream, first, scale, offset));
+    HIP_OK(h, launch_fill_normal(lc(h, -1), dst_dev, dtype, n, seed, stream, first, scale, offset));
     return 1;
 }
 

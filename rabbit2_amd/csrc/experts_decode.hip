@@ -1,0 +1,288 @@
+// Expert FFN for decode and small batches, specialised for the common shapes: every row length is
+// a whole number of 1 KiB wave-steps (D and H multiples of 512 bf16 or 256 f32, at most 8 steps),
+// so each wavefront knows its exact load list at compile time and issues all of it before the
+// first wait. The generic kernels in experts_gemv.hip cover every other shape.
+//
+// Reference: rabbit2/src/rabbit2.c:531-541 (per selected expert: h1 = W1 xb, h3 = W3 xb,
+// h = silu(h1) * h3, tmp = W2 h, moe += w_k * tmp in selection order; x += moe at :542), experts in
+// the .rbt2 blob layout w1[H][D] | w3[H][D] | w2[D][H] (rabbit2.c:173, rbt2.py:152-156).
+//
+// gateup: one wave per JW consecutive hidden units j of one (token, slot) pair; per lane 2*JW*NC
+//   16-byte weight loads + NC x loads, then 2*JW wave sums; h[p][j] = silu(g)*u in f32.
+// down:   one block per (token, 4*RW output rows); the token's K hidden vectors are staged once in
+//   LDS; per wave, KC slots x RW rows x NH 16-byte weight loads in flight, then the K dot products
+//   are combined in selection order exactly like the engine's loop.
+// Bytes per decode layer at the OLMoE shape: gateup 64 MiB of weights, down 32 MiB.
+#include <math.h>
+
+#include "rbt2_internal.h"
+
+namespace rbt {
+namespace {
+
+template <int DT>
+struct Elem {
+    static constexpr int kEsz = DT == RBT_DT_F32 ? 4 : 2;
+    static constexpr int kPer = 16 / kEsz;  // weights per 16-byte load
+};
+
+// dot of 16 bytes of weights with the matching kPer floats of x
+template <int DT>
+__device__ __forceinline__ float dot16(const u32x4 w, const float *x) {
+    if constexpr (DT == RBT_DT_BF16) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(x);
+        const f32x4 x1 = *reinterpret_cast<const f32x4 *>(x + 4);
+        return bf16_lo(w.x) * x0.x + bf16_hi(w.x) * x0.y + bf16_lo(w.y) * x0.z + bf16_hi(w.y) * x0.w +
+               bf16_lo(w.z) * x1.x + bf16_hi(w.z) * x1.y + bf16_lo(w.w) * x1.z + bf16_hi(w.w) * x1.w;
+    } else {
+        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(x);
+        return __uint_as_float(w.x) * x0.x + __uint_as_float(w.y) * x0.y + __uint_as_float(w.z) * x0.z +
+               __uint_as_float(w.w) * x0.w;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float dot16r(const u32x4 w, const f32x4 x0, const f32x4 x1) {
+    if constexpr (DT == RBT_DT_BF16) {
+        return bf16_lo(w.x) * x0.x + bf16_hi(w.x) * x0.y + bf16_lo(w.y) * x0.z + bf16_hi(w.y) * x0.w +
+               bf16_lo(w.z) * x1.x + bf16_hi(w.z) * x1.y + bf16_lo(w.w) * x1.z + bf16_hi(w.w) * x1.w;
+    } else {
+        (void)x1;
+        return __uint_as_float(w.x) * x0.x + __uint_as_float(w.y) * x0.y + __uint_as_float(w.z) * x0.z +
+               __uint_as_float(w.w) * x0.w;
+    }
+}
+
+// grid: ceil(P*H/JW / 4) blocks of 4 waves; requires H % JW == 0 and D == NC * 64 * kPer.
+template <int DT, int NC, int JW>
+__global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
+                                                          const int32_t *__restrict__ routing,
+                                                          const float *__restrict__ xb, int K, int H,
+                                                          long long items, float *__restrict__ hbuf) {
+    constexpr int kEsz = Elem<DT>::kEsz, kPer = Elem<DT>::kPer;
+    constexpr int D = NC * kWave * kPer;
+    const int lane = threadIdx.x & (kWave - 1);
+    const long long item = (long long)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+    if (item >= items) return;
+    const long long row0 = item * JW;
+    const long long p = row0 / H;
+    const int j0 = (int)(row0 - p * H);
+    const int e = routing[p];
+    const int t = (int)(p / K);
+    const uint8_t *w1 = experts + (size_t)e * stride + (size_t)j0 * D * kEsz;
+    const uint8_t *w3 = w1 + (size_t)H * D * kEsz;
+    const float *x = xb + (size_t)t * D;
+
+    u32x4 a[JW][NC], b[JW][NC];
+    f32x4 x0[NC], x1[NC];
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj)
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const size_t off = ((size_t)jj * D + (size_t)(lane + kWave * i) * kPer) * kEsz;
+            a[jj][i] = ld_stream_u4(w1 + off);
+            b[jj][i] = ld_stream_u4(w3 + off);
+        }
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const float *xp = x + (lane + kWave * i) * kPer;
+        x0[i] = *reinterpret_cast<const f32x4 *>(xp);
+        if constexpr (DT == RBT_DT_BF16) x1[i] = *reinterpret_cast<const f32x4 *>(xp + 4);
+    }
+    // keep the scheduler from sinking the loads next to their uses: all of them go out first
+    __builtin_amdgcn_sched_barrier(0);
+    float g[JW], u[JW];
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
+        g[jj] = 0.0f;
+        u[jj] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            g[jj] += dot16r<DT>(a[jj][i], x0[i], x1[i]);
+            u[jj] += dot16r<DT>(b[jj][i], x0[i], x1[i]);
+        }
+    }
+#pragma unroll
+    for (int jj = 0; jj < JW; ++jj) {
+        const float gs = wave_sum(g[jj]), us = wave_sum(u[jj]);
+        if (lane == jj) hbuf[(size_t)p * H + j0 + jj] = (gs / (1.0f + expf(-gs))) * us;
+    }
+}
+
+// grid (ceil(D / (4*RW)), T), block 256, dynamic LDS K*H*4 bytes; requires H == NH * 64 * kPer.
+template <int DT, int NH, int RW>
+__global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
+                                                        const int32_t *__restrict__ routing,
+                                                        const float *__restrict__ weights,
+                                                        const float *__restrict__ hbuf, int K, int D,
+                                                        float *__restrict__ x_inout, float *__restrict__ moe_out) {
+    constexpr int kEsz = Elem<DT>::kEsz, kPer = Elem<DT>::kPer;
+    constexpr int H = NH * kWave * kPer;
+    constexpr int KC = NH <= 2 ? 8 : 4;  // slots whose loads are in flight together (<= 32 per lane)
+    extern __shared__ __align__(16) float hs[];  // [K][H]
+    __shared__ float s_w[64];
+    const int t = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+
+    const int d0 = (blockIdx.x * (blockDim.x / kWave) + wv) * RW;
+    const bool active = d0 < D;
+    const int dbase = active ? d0 : 0;  // inactive waves still help stage h; their loads stay in range
+    const int nr = D - dbase < RW ? D - dbase : RW;
+    const int32_t *rt = routing + (size_t)t * K;
+
+    // The weight loads of the first slot chunk go out first: they only need the expert ids, so
+    // they are in flight while h is staged.
+    u32x4 w[KC][RW][NH];
+    auto load_chunk = [&](int k0, int nk) {
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+            const int slot = k0 + (kk < nk ? kk : 0);  // clamped: always a valid expert row
+            const uint8_t *base = experts + (size_t)rt[slot] * stride + 2 * (size_t)H * D * kEsz;
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                const int d = dbase + (r < nr ? r : 0);
+#pragma unroll
+                for (int i = 0; i < NH; ++i)
+                    w[kk][r][i] = ld_stream_u4(base + ((size_t)d * H + (size_t)(lane + kWave * i) * kPer) * kEsz);
+            }
+        }
+    };
+    load_chunk(0, K < KC ? K : KC);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // stage h of this token: K*H/4 16-byte units, 8 in flight per thread
+    {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(hbuf + (size_t)t * K * H);
+        f32x4 *dst = reinterpret_cast<f32x4 *>(hs);
+        const int units = K * H / 4;
+        for (int b0 = tid; b0 < units; b0 += blockDim.x * 8) {
+            f32x4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = src[min(b0 + i * (int)blockDim.x, units - 1)];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (b0 + i * (int)blockDim.x < units) dst[b0 + i * blockDim.x] = v[i];
+        }
+    }
+    if (tid < K) s_w[tid] = weights[(size_t)t * K + tid];
+    __syncthreads();
+    if (!active) return;  // no barrier follows
+
+    float moe[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) moe[r] = 0.0f;
+
+    for (int k0 = 0; k0 < K; k0 += KC) {
+        const int nk = K - k0 < KC ? K - k0 : KC;
+        if (k0 > 0) {
+            load_chunk(k0, nk);
+            __builtin_amdgcn_sched_barrier(0);  // every weight load of the chunk is issued before any use
+        }
+        float acc[KC][RW];
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+            const float *hk = hs + (size_t)(k0 + (kk < nk ? kk : 0)) * H;
+#pragma unroll
+            for (int r = 0; r < RW; ++r) acc[kk][r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NH; ++i) {
+                const float *hp = hk + (lane + kWave * i) * kPer;
+#pragma unroll
+                for (int r = 0; r < RW; ++r) acc[kk][r] += dot16<DT>(w[kk][r][i], hp);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r) acc[kk][r] = wave_sum(acc[kk][r]);
+        }
+        for (int kk = 0; kk < nk; ++kk) {
+            const float wk = s_w[k0 + kk];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+#pragma clang fp contract(off)
+                moe[r] = moe[r] + wk * acc[kk][r];  // rabbit2.c:540, rounded product then add
+            }
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            if (r < nr) {
+                const size_t o = (size_t)t * D + d0 + r;
+                if (moe_out) moe_out[o] = moe[r];
+                if (x_inout) x_inout[o] = x_inout[o] + moe[r];
+            }
+        }
+    }
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int DT, int NC>
+hipError_t gateup_nc(const Launch &L, const uint8_t *E, uint64_t stride, const int32_t *routing, const float *xb,
+                     int T, int K, int H, float *hbuf) {
+    constexpr int JW = 2;
+    const long long items = (long long)T * K * H / JW;
+    return launch(L, gateup_fast_kernel<DT, NC, JW>, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, E, stride,
+                  routing, xb, K, H, items, hbuf);
+}
+
+template <int DT, int NH>
+hipError_t down_nh(const Launch &L, const uint8_t *E, uint64_t stride, const int32_t *routing, const float *weights,
+                   const float *hbuf, int T, int K, int D, float *x_inout, float *moe_out) {
+    constexpr int RW = 2;
+    constexpr int H = NH * kWave * Elem<DT>::kPer;
+    return launch(L, down_fast_kernel<DT, NH, RW>, dim3((unsigned)((D + 4 * RW - 1) / (4 * RW)), (unsigned)T),
+                  dim3(256), (uint32_t)((size_t)K * H * 4), E, stride, routing, weights, hbuf, K, D, x_inout,
+                  moe_out);
+}
+
+template <int DT>
+hipError_t decode_dt(const Launch &Lg, const Launch &Ld, const uint8_t *E, uint64_t stride, const int32_t *routing,
+                     const float *weights, const float *xb, float *hbuf, int T, int K, int D, int H, float *x_inout,
+                     float *moe_out) {
+    constexpr int step = kWave * Elem<DT>::kPer;
+    const int nc = D / step, nh = H / step;
+    hipError_t e;
+    switch (nc) {
+        case 1: e = gateup_nc<DT, 1>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        case 2: e = gateup_nc<DT, 2>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        case 3: e = gateup_nc<DT, 3>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        case 4: e = gateup_nc<DT, 4>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        case 6: e = gateup_nc<DT, 6>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        case 8: e = gateup_nc<DT, 8>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        default: return hipErrorNotSupported;
+    }
+    if (e != hipSuccess) return e;
+    switch (nh) {
+        case 1: return down_nh<DT, 1>(Ld, E, stride, routing, weights, hbuf, T, K, D, x_inout, moe_out);
+        case 2: return down_nh<DT, 2>(Ld, E, stride, routing, weights, hbuf, T, K, D, x_inout, moe_out);
+        case 3: return down_nh<DT, 3>(Ld, E, stride, routing, weights, hbuf, T, K, D, x_inout, moe_out);
+        case 4: return down_nh<DT, 4>(Ld, E, stride, routing, weights, hbuf, T, K, D, x_inout, moe_out);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace
+
+bool experts_decode_supported(int dtype, int T, int K, int D, int H, const void *experts, uint64_t stride,
+                              const float *xb, const float *hbuf) {
+    const int step = dtype == RBT_DT_BF16 ? 512 : 256;
+    const int nc = D / step, nh = H / step;
+    const bool nc_ok = D % step == 0 && (nc == 1 || nc == 2 || nc == 3 || nc == 4 || nc == 6 || nc == 8);
+    const bool nh_ok = H % step == 0 && nh >= 1 && nh <= 4;
+    return nc_ok && nh_ok && H % 2 == 0 && T >= 1 && T <= 65535 && (size_t)K * H * 4 <= 64 * 1024 &&
+           aligned16(experts) && stride % 16 == 0 && aligned16(xb) && aligned16(hbuf);
+}
+
+hipError_t launch_experts_decode(const Launch &Lg, const Launch &Ld, int dtype, const void *experts, uint64_t stride,
+                                 const int32_t *routing, const float *weights, const float *xb, float *hbuf, int T,
+                                 int K, int D, int H, float *x_inout, float *moe_out) {
+    const uint8_t *E = static_cast<const uint8_t *>(experts);
+    return dtype == RBT_DT_BF16
+               ? decode_dt<RBT_DT_BF16>(Lg, Ld, E, stride, routing, weights, xb, hbuf, T, K, D, H, x_inout, moe_out)
+               : decode_dt<RBT_DT_F32>(Lg, Ld, E, stride, routing, weights, xb, hbuf, T, K, D, H, x_inout, moe_out);
+}
+
+}  // namespace rbt

@@ -173,7 +173,7 @@ inline unsigned blocks_for(long long rows) { return (unsigned)((rows + 3) / 4); 
 
 }  // namespace
 
-hipError_t launch_gateup_gemv(hipStream_t s, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
+hipError_t launch_gateup_gemv(const Launch &L, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
                               const float *xb, int T, int K, int D, int H, float *hbuf) {
     const long long rows = (long long)T * K * H;
     if (rows == 0) return hipSuccess;
@@ -182,23 +182,23 @@ hipError_t launch_gateup_gemv(hipStream_t s, int dtype, const void *experts, uin
     const dim3 g(blocks_for(rows)), b(256);
     if (dtype == RBT_DT_BF16) {
         if (vec)
-            hipLaunchKernelGGL((gateup_gemv_kernel<RBT_DT_BF16, true>), g, b, 0, s, E, stride, routing, xb, K, D, H,
+            return launch(L, gateup_gemv_kernel<RBT_DT_BF16, true>, g, b, 0, E, stride, routing, xb, K, D, H,
                                rows, hbuf);
         else
-            hipLaunchKernelGGL((gateup_gemv_kernel<RBT_DT_BF16, false>), g, b, 0, s, E, stride, routing, xb, K, D, H,
+            return launch(L, gateup_gemv_kernel<RBT_DT_BF16, false>, g, b, 0, E, stride, routing, xb, K, D, H,
                                rows, hbuf);
     } else {
         if (vec)
-            hipLaunchKernelGGL((gateup_gemv_kernel<RBT_DT_F32, true>), g, b, 0, s, E, stride, routing, xb, K, D, H,
+            return launch(L, gateup_gemv_kernel<RBT_DT_F32, true>, g, b, 0, E, stride, routing, xb, K, D, H,
                                rows, hbuf);
         else
-            hipLaunchKernelGGL((gateup_gemv_kernel<RBT_DT_F32, false>), g, b, 0, s, E, stride, routing, xb, K, D, H,
+            return launch(L, gateup_gemv_kernel<RBT_DT_F32, false>, g, b, 0, E, stride, routing, xb, K, D, H,
                                rows, hbuf);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_down_combine(hipStream_t s, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
+hipError_t launch_down_combine(const Launch &L, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
                                const float *weights, const float *hbuf, int T, int K, int D, int H, float *x_inout,
                                float *moe_out) {
     const long long rows = (long long)T * D;
@@ -208,37 +208,33 @@ hipError_t launch_down_combine(hipStream_t s, int dtype, const void *experts, ui
     const dim3 g(blocks_for(rows)), b(256);
     if (dtype == RBT_DT_BF16) {
         if (vec)
-            hipLaunchKernelGGL((down_combine_kernel<RBT_DT_BF16, true>), g, b, 0, s, E, stride, routing, weights, hbuf,
-                               K, D, H, rows, x_inout, moe_out);
-        else
-            hipLaunchKernelGGL((down_combine_kernel<RBT_DT_BF16, false>), g, b, 0, s, E, stride, routing, weights, hbuf,
-                               K, D, H, rows, x_inout, moe_out);
-    } else {
-        if (vec)
-            hipLaunchKernelGGL((down_combine_kernel<RBT_DT_F32, true>), g, b, 0, s, E, stride, routing, weights, hbuf,
-                               K, D, H, rows, x_inout, moe_out);
-        else
-            hipLaunchKernelGGL((down_combine_kernel<RBT_DT_F32, false>), g, b, 0, s, E, stride, routing, weights, hbuf,
-                               K, D, H, rows, x_inout, moe_out);
+            return launch(L, down_combine_kernel<RBT_DT_BF16, true>, g, b, 0, E, stride, routing, weights, hbuf, K, D,
+                          H, rows, x_inout, moe_out);
+        return launch(L, down_combine_kernel<RBT_DT_BF16, false>, g, b, 0, E, stride, routing, weights, hbuf, K, D, H,
+                      rows, x_inout, moe_out);
     }
-    return hipGetLastError();
+    if (vec)
+        return launch(L, down_combine_kernel<RBT_DT_F32, true>, g, b, 0, E, stride, routing, weights, hbuf, K, D, H,
+                      rows, x_inout, moe_out);
+    return launch(L, down_combine_kernel<RBT_DT_F32, false>, g, b, 0, E, stride, routing, weights, hbuf, K, D, H, rows,
+                  x_inout, moe_out);
 }
 
-hipError_t launch_matvec(hipStream_t s, int dtype, const void *W, const float *x, float *out, int rows, int cols) {
+hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols) {
     if (rows <= 0) return hipSuccess;
     const bool vec = vec_ok(dtype, cols) && aligned16(W) && aligned16(x);
     const uint8_t *Wb = static_cast<const uint8_t *>(W);
     const dim3 g(blocks_for(rows)), b(256);
     if (dtype == RBT_DT_BF16) {
         if (vec)
-            hipLaunchKernelGGL((matvec_kernel<RBT_DT_BF16, true>), g, b, 0, s, Wb, x, out, rows, cols);
+            return launch(L, matvec_kernel<RBT_DT_BF16, true>, g, b, 0, Wb, x, out, rows, cols);
         else
-            hipLaunchKernelGGL((matvec_kernel<RBT_DT_BF16, false>), g, b, 0, s, Wb, x, out, rows, cols);
+            return launch(L, matvec_kernel<RBT_DT_BF16, false>, g, b, 0, Wb, x, out, rows, cols);
     } else {
         if (vec)
-            hipLaunchKernelGGL((matvec_kernel<RBT_DT_F32, true>), g, b, 0, s, Wb, x, out, rows, cols);
+            return launch(L, matvec_kernel<RBT_DT_F32, true>, g, b, 0, Wb, x, out, rows, cols);
         else
-            hipLaunchKernelGGL((matvec_kernel<RBT_DT_F32, false>), g, b, 0, s, Wb, x, out, rows, cols);
+            return launch(L, matvec_kernel<RBT_DT_F32, false>, g, b, 0, Wb, x, out, rows, cols);
     }
     return hipGetLastError();
 }

@@ -61,16 +61,15 @@ __global__ void fill_normal_kernel(void *dst, int dtype, uint64_t n, uint64_t ke
 
 }  // namespace
 
-hipError_t launch_fill_normal(hipStream_t s, void *dst, int dtype, uint64_t n, uint64_t seed, uint64_t stream,
+hipError_t launch_fill_normal(const Launch &L, void *dst, int dtype, uint64_t n, uint64_t seed, uint64_t stream,
                               uint64_t first, float scale, float offset) {
     if (n == 0) return hipSuccess;
     const uint64_t key = mix64((seed ^ (stream * kGolden)) + kGolden);
     const uint64_t pairs = (n + 2) / 2;
     uint64_t blocks = (pairs + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, s, dst, dtype, n, key, first, scale,
-                       offset);
-    return hipGetLastError();
+    return launch(L, fill_normal_kernel, dim3((unsigned)blocks), dim3(256), 0, dst, dtype, n, key, first, scale,
+                  offset);
 }
 
 }  // namespace rbt

@@ -1,6 +1,7 @@
 // Internal declarations shared by the gfx950 kernels and the C-ABI layer (not installed).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -42,27 +43,49 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Where and how a kernel is launched: the stream, and optionally a pair of events that the runtime
+// stamps with the kernel's own start and end (hipExtLaunchKernel), used by the profiling mode.
+struct Launch {
+    hipStream_t s = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
+template <typename F, typename... Args>
+inline hipError_t launch(const Launch &L, F kernel, dim3 grid, dim3 block, uint32_t shmem, Args... args) {
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, L.s, L.start, L.stop, 0, args...);
+    return hipGetLastError();
+}
+
 // ---- launchers (each returns hipSuccess or the launch error) ----
 
-// Router logits in the engine's exact order + softmax + top-k + combine weights, one token per
-// grid row; the last block of each token finishes the softmax/top-k (counters[t] must be 0 on
-// entry and are left 0). probs: [T][E] workspace.
-hipError_t launch_router(hipStream_t s, int order, int dtype, const float *xb, const void *W, const float *bias, int T,
-                         int E, int D, int K, int norm_topk, float *probs, unsigned *counters, int32_t *routing,
-                         float *weights);
+// Router logits in the engine's exact order (logits kernel, launch context L), then softmax + top-k +
+// combine weights (one block per token, context Lk). probs: [T][E] workspace (logits, then
+// probabilities).
+hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype, const float *xb, const void *W,
+                         const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,
+                         int32_t *routing, float *weights);
 
 // Per-(token, slot) GEMV form of the expert FFN (decode and small batches).
-hipError_t launch_gateup_gemv(hipStream_t s, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
+hipError_t launch_gateup_gemv(const Launch &L, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
                               const float *xb, int T, int K, int D, int H, float *hbuf);
-hipError_t launch_down_combine(hipStream_t s, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
+hipError_t launch_down_combine(const Launch &L, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
                                const float *weights, const float *hbuf, int T, int K, int D, int H, float *x_inout,
                                float *moe_out);
 
+// The same expert FFN specialised for whole-wave-step row lengths (the OLMoE shape among them):
+// every load of a wave is issued before the first wait. Lg/Ld: launch contexts of the gate/up and
+// down kernels.
+bool experts_decode_supported(int dtype, int T, int K, int D, int H, const void *experts, uint64_t stride,
+                              const float *xb, const float *hbuf);
+hipError_t launch_experts_decode(const Launch &Lg, const Launch &Ld, int dtype, const void *experts, uint64_t stride,
+                                 const int32_t *routing, const float *weights, const float *xb, float *hbuf, int T,
+                                 int K, int D, int H, float *x_inout, float *moe_out);
+
 // Dense matvec (one row per wave).
-hipError_t launch_matvec(hipStream_t s, int dtype, const void *W, const float *x, float *out, int rows, int cols);
+hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);
 
 // Synthetic normal fill (SplitMix64 + Box-Muller), see rbt_hip_fill_normal.
-hipError_t launch_fill_normal(hipStream_t s, void *dst, int dtype, uint64_t n, uint64_t seed, uint64_t stream,
+hipError_t launch_fill_normal(const Launch &L, void *dst, int dtype, uint64_t n, uint64_t seed, uint64_t stream,
                               uint64_t first, float scale, float offset);
 
 }  // namespace rbt

@@ -13,8 +13,12 @@
 //                    the < 16-column tail in order.
 //   RBT_ORDER_SCALAR (rabbit2.c:356-390): 4 chains over columns 4m+j, tail into chain 0, result
 //                    (s0+s1)+(s2+s3).
-// Each chain is one thread: the work is D/16 (or D/4) dependent adds per thread, and a token's
-// E rows are spread over ceil(E/rows_per_block) blocks so the router bytes stream through many CUs.
+// Each chain is one thread. A block owns `rpb` router rows of one token; their columns are staged
+// through LDS a chunk at a time with 16-byte loads (every load of a chunk in flight at once), and
+// the chains then run out of LDS. A token's E rows are spread over ceil(E/rpb) blocks so the 256 KiB
+// router streams through many CUs. A second kernel (one block per token) does the softmax and the
+// top-k; the kernel boundary is the only synchronisation (no device-scope fences or atomics, whose
+// L2 write-back/invalidate costs more than a launch inside a graph).
 // No multiply-add contraction anywhere in this file: every product is rounded before its add,
 // exactly as the engine's `-std=c99` build does.
 #pragma clang fp contract(off)
@@ -27,6 +31,26 @@ namespace rbt {
 namespace {
 
 constexpr int kLdsProbsMax = 4096;  // tokens with E <= this keep probabilities in LDS
+constexpr int kRankMax = 1024;      // top-k by rank counting up to this many experts
+constexpr int kPad = 16;            // elements of padding per staged row (spreads rows over LDS banks)
+
+// WIDE: blocks of at most 4 rows stage 2048 columns per chunk (one round trip for the OLMoE
+// width); blocks of up to 16 rows stage 1024 (bf16) / 512 (f32), keeping LDS under 40 KiB.
+template <int DT, bool WIDE = false>
+struct RouterTile {
+    using W = typename std::conditional<DT == RBT_DT_F32, float, uint16_t>::type;
+    static constexpr int kCols = WIDE ? 2048 : (DT == RBT_DT_F32 ? 512 : 1024);  // multiple of 16
+    static constexpr int kPitch = kCols + kPad;
+    static constexpr int kEsz = (int)sizeof(W);
+};
+
+template <int DT>
+__device__ __forceinline__ float widen(typename RouterTile<DT, false>::W w) {
+    if constexpr (DT == RBT_DT_F32)
+        return w;
+    else
+        return __uint_as_float((uint32_t)w << 16);
+}
 
 __device__ float block_max_f(float v, float *red) {
 #pragma unroll
@@ -59,70 +83,125 @@ __device__ unsigned long long block_max_u64(unsigned long long v, unsigned long 
     return r;
 }
 
-// grid (ceil(E/rpb), T), block rpb*NCH threads (a multiple of 64, at most 256).
-template <int NCH, int DT>
-__global__ __launch_bounds__(256) void router_kernel(const float *__restrict__ xb, const void *__restrict__ W,
-                                                     const float *__restrict__ bias, int E, int D, int K,
-                                                     int norm_topk, int rpb, float *__restrict__ probs,
-                                                     unsigned *__restrict__ counters, int32_t *__restrict__ routing,
-                                                     float *__restrict__ weights) {
-    extern __shared__ float smem[];  // max(blockDim, E<=kLdsProbsMax ? E : 0) floats
-    __shared__ float red_f[4];
-    __shared__ unsigned long long red_u[4];
-    __shared__ int s_last;
-    __shared__ int32_t s_idx[64];
-    __shared__ float s_wt[64];
-    __shared__ float s_sum;
+// grid (ceil(E/rpb), T); block rpb*NCH threads (64 or 256). Dynamic LDS (host computes the size):
+//   wt [rpb][kPitch] W | xt [kCols] f32 | part [blockDim] f32
+template <int NCH, int DT, bool WIDE>
+__global__ __launch_bounds__(256) void router_logits_kernel(const float *__restrict__ xb,
+                                                            const void *__restrict__ Wv,
+                                                            const float *__restrict__ bias, int E, int D, int rpb,
+                                                            int vec, float *__restrict__ logits) {
+    using Tile = RouterTile<DT, WIDE>;
+    using W = typename Tile::W;
+    extern __shared__ __align__(16) unsigned char smem[];
+    W *wt = reinterpret_cast<W *>(smem);
+    float *xt = reinterpret_cast<float *>(smem + (size_t)rpb * Tile::kPitch * Tile::kEsz);
+    float *part = xt + Tile::kCols;
 
+    const W *Wg = static_cast<const W *>(Wv);
     const int t = blockIdx.y;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, nt = blockDim.x;
     const int rr = tid / NCH, c = tid - rr * NCH;
-    const int r = blockIdx.x * rpb + rr;
+    const int r0 = blockIdx.x * rpb;
+    const int nrows = E - r0 < rpb ? E - r0 : rpb;
     const float *x = xb + (size_t)t * D;
-    float *prow = probs + (size_t)t * E;
+    float *prow = logits + (size_t)t * E;
     const int nfull = D / NCH;
+    const int body = nfull * NCH;  // columns the chains cover; the rest is the tail
 
-    // ---- one chain per thread
+    // ---- chains over LDS-staged chunks (chunk boundaries are multiples of NCH, so each chain's
+    // column order is unchanged)
     float acc = 0.0f;
-    if (r < E) {
-        const size_t rb = (size_t)r * D;
-#pragma unroll 8
-        for (int m = 0; m < nfull; ++m) {
-            const int col = m * NCH + c;
-            acc = acc + load_w<DT>(W, rb + col) * x[col];
+    for (int c0 = 0; c0 < body; c0 += Tile::kCols) {
+        const int cn = body - c0 < Tile::kCols ? body - c0 : Tile::kCols;
+        if (vec) {
+            // 16-byte units: rows are 16-byte aligned and cn*esz is a multiple of 16 (host-checked).
+            // Addresses are clamped into range so every load of a batch is issued before any wait.
+            constexpr int per = 16 / Tile::kEsz;
+            constexpr int UB = 16;  // 4 rows x 2048 bf16 by 64 threads: one batch
+            const int upr = cn / per, total = nrows * upr;
+            for (int b0 = tid; b0 < total; b0 += nt * UB) {
+                u32x4 v[UB];
+#pragma unroll
+                for (int i = 0; i < UB; ++i) {
+                    const int u = min(b0 + i * nt, total - 1);
+                    const int rl = u / upr, k = u - rl * upr;
+                    v[i] = *reinterpret_cast<const u32x4 *>(Wg + (size_t)(r0 + rl) * D + c0 + k * per);
+                }
+#pragma unroll
+                for (int i = 0; i < UB; ++i) {
+                    const int u = b0 + i * nt;
+                    if (u < total) {
+                        const int rl = u / upr, k = u - rl * upr;
+                        *reinterpret_cast<u32x4 *>(wt + rl * Tile::kPitch + k * per) = v[i];
+                    }
+                }
+            }
+            const int xu = cn / 4;
+            for (int b0 = tid; b0 < xu; b0 += nt * 4) {
+                f32x4 v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4 *>(x + c0 + 4 * min(b0 + i * nt, xu - 1));
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (b0 + i * nt < xu) *reinterpret_cast<f32x4 *>(xt + 4 * (b0 + i * nt)) = v[i];
+            }
+        } else {
+            for (int i = tid; i < nrows * cn; i += nt) {
+                const int rl = i / cn, cc = i - rl * cn;
+                wt[rl * Tile::kPitch + cc] = Wg[(size_t)(r0 + rl) * D + c0 + cc];
+            }
+            for (int i = tid; i < cn; i += nt) xt[i] = x[c0 + i];
         }
+        __syncthreads();
+        if (rr < nrows) {
+            const W *wr = wt + rr * Tile::kPitch;
+            const int steps = cn / NCH;
+#pragma unroll 8
+            for (int m = 0; m < steps; ++m) {
+                const int cc = m * NCH + c;
+                acc = acc + widen<DT>(wr[cc]) * xt[cc];
+            }
+        }
+        __syncthreads();
     }
-    smem[tid] = acc;
+    part[tid] = acc;
     __syncthreads();
-    if (c == 0 && r < E) {
-        const size_t rb = (size_t)r * D;
+    if (c == 0 && rr < nrows) {
+        const int r = r0 + rr;
+        const W *wrow = Wg + (size_t)r * D;
         float res;
         if constexpr (NCH == 16) {
             float sum = 0.0f;
-            for (int j = 0; j < 8; ++j) sum = sum + (smem[tid + j] + smem[tid + 8 + j]);
-            for (int i = nfull * 16; i < D; ++i) sum = sum + load_w<DT>(W, rb + i) * x[i];
+            for (int j = 0; j < 8; ++j) sum = sum + (part[tid + j] + part[tid + 8 + j]);
+            for (int i = body; i < D; ++i) sum = sum + widen<DT>(wrow[i]) * x[i];
             res = sum;
         } else {
-            float s0 = smem[tid], s1 = smem[tid + 1], s2 = smem[tid + 2], s3 = smem[tid + 3];
-            for (int i = nfull * 4; i < D; ++i) s0 = s0 + load_w<DT>(W, rb + i) * x[i];
+            float s0 = part[tid], s1 = part[tid + 1], s2 = part[tid + 2], s3 = part[tid + 3];
+            for (int i = body; i < D; ++i) s0 = s0 + widen<DT>(wrow[i]) * x[i];
             res = (s0 + s1) + (s2 + s3);
         }
         if (bias) res = res + bias[r];
         prow[r] = res;
     }
 
-    // ---- the last block of this token to finish does softmax + top-k (no spinning: the others exit)
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&counters[t], 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+}
 
-    const int nt = blockDim.x;
+// grid (T), block 64 or 256 threads; dynamic LDS E floats when E <= kLdsProbsMax. Reads the logits
+// row of its token, leaves the probabilities in it, writes routing/weights.
+__global__ __launch_bounds__(256) void router_topk_kernel(int E, int K, int norm_topk, float *__restrict__ probs,
+                                                          int32_t *__restrict__ routing,
+                                                          float *__restrict__ weights) {
+    extern __shared__ __align__(16) float pb_lds[];
+    __shared__ float red_f[4];
+    __shared__ unsigned long long red_u[4];
+    __shared__ int32_t s_idx[64];
+    __shared__ float s_wt[64];
+    __shared__ float s_sum;
+    const int t = blockIdx.x;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    float *prow = probs + (size_t)t * E;
     const bool lds = E <= kLdsProbsMax;
-    float *pb = lds ? smem : prow;
-    __syncthreads();  // smem held the chain partials until here
+    float *pb = lds ? pb_lds : prow;
     float mx = -INFINITY;
     for (int i = tid; i < E; i += nt) {
         const float v = prow[i];
@@ -134,14 +213,27 @@ __global__ __launch_bounds__(256) void router_kernel(const float *__restrict__ x
     const float first = pb[0];
     if (first != first) mx = first;  // ... except that a NaN in element 0 is its starting maximum
     for (int i = tid; i < E; i += nt) {
-        // expf rounded correctly from a double evaluation (glibc's expf is within 0.502 ulp)
+        // expf rounded from a double evaluation: within 0.5 ulp + 2^-29, as glibc's expf (0.502 ulp)
         pb[i] = (float)exp((double)(pb[i] - mx));
     }
     if (!lds) __threadfence();
     __syncthreads();
     if (tid == 0) {
+        // the engine's sequential order; 16-byte LDS reads keep several values in flight
         float sum = 0.0f;
-        for (int i = 0; i < E; ++i) sum = sum + pb[i];  // the engine's sequential order
+        int i = 0;
+        if (lds) {
+            const f32x4 *p4 = reinterpret_cast<const f32x4 *>(pb);
+#pragma unroll 4
+            for (; i + 4 <= E; i += 4) {
+                const f32x4 v = p4[i / 4];
+                sum = sum + v.x;
+                sum = sum + v.y;
+                sum = sum + v.z;
+                sum = sum + v.w;
+            }
+        }
+        for (; i < E; ++i) sum = sum + pb[i];
         s_sum = sum;
     }
     __syncthreads();
@@ -155,6 +247,21 @@ __global__ __launch_bounds__(256) void router_kernel(const float *__restrict__ x
         if (tid < K) {
             s_idx[tid] = tid;
             s_wt[tid] = pb[tid];
+        }
+    } else if (lds && E <= kRankMax) {
+        // The engine's K rounds of "largest unused, lowest index on ties" are the first K places of a
+        // stable descending sort: an element's place is the number of elements that beat it.
+        for (int i = tid; i < E; i += nt) {
+            const float pi = pb[i];
+            int rank = 0;
+            for (int j = 0; j < E; ++j) {
+                const float pj = pb[j];
+                rank += (pj > pi) | ((pj == pi) & (j < i));
+            }
+            if (rank < K) {
+                s_idx[rank] = i;
+                s_wt[rank] = pi;
+            }
         }
     } else {
         // probabilities are >= +0, so their bit patterns order like the values; the low word makes
@@ -185,37 +292,54 @@ __global__ __launch_bounds__(256) void router_kernel(const float *__restrict__ x
             routing[(size_t)t * K + j] = s_idx[j];
             weights[(size_t)t * K + j] = norm_topk ? s_wt[j] / wsum : s_wt[j];
         }
-        counters[t] = 0u;  // ready for the next launch
     }
+    if (lds)
+        for (int i = tid; i < E; i += nt) prow[i] = pb[i];
+}
+
+template <int NCH, int DT, bool WIDE>
+hipError_t launch_logits(const Launch &L, const float *xb, const void *W, const float *bias, int T, int E, int D,
+                         int threads, float *probs) {
+    using Tile = RouterTile<DT, WIDE>;
+    const int rpb = threads / NCH;
+    const bool vec = (reinterpret_cast<uintptr_t>(W) % 16 == 0) && ((size_t)D * Tile::kEsz) % 16 == 0 &&
+                     (reinterpret_cast<uintptr_t>(xb) % 16 == 0) && D % 16 == 0;
+    const size_t lds = (size_t)rpb * Tile::kPitch * Tile::kEsz + Tile::kCols * 4 + threads * 4;
+    return launch(L, router_logits_kernel<NCH, DT, WIDE>, dim3((E + rpb - 1) / rpb, T), dim3(threads),
+                  (uint32_t)lds, xb, W, bias, E, D, rpb, vec ? 1 : 0, probs);
 }
 
 template <int NCH, int DT>
-hipError_t launch_t(hipStream_t s, const float *xb, const void *W, const float *bias, int T, int E, int D, int K,
-                    int norm_topk, float *probs, unsigned *counters, int32_t *routing, float *weights) {
-    // Small batches: 64-thread blocks (4 or 16 rows) so even one token spreads over E/rpb CUs.
-    const int threads = T <= 8 ? 64 : 256;
-    const int rpb = threads / NCH;
-    const dim3 grid((E + rpb - 1) / rpb, T);
-    const int lds_floats = E <= kLdsProbsMax ? (E > threads ? E : threads) : threads;
-    hipLaunchKernelGGL((router_kernel<NCH, DT>), grid, dim3(threads), lds_floats * sizeof(float), s, xb, W, bias, E,
-                       D, K, norm_topk, rpb, probs, counters, routing, weights);
-    return hipGetLastError();
+hipError_t launch_t(const Launch &L, const Launch &Lk, const float *xb, const void *W, const float *bias, int T, int E,
+                    int D, int K, int norm_topk, float *probs, int32_t *routing, float *weights) {
+    // 64-thread blocks for small batches (4 or 16 rows each, so one token's router spreads over many
+    // CUs); 256 threads (16 rows) for larger batches with the AVX2 order.
+    const int threads = (NCH == 16 && T > 8) ? 256 : 64;
+    const bool wide = threads / NCH <= 4;
+    hipError_t e = wide ? launch_logits<NCH, DT, true>(L, xb, W, bias, T, E, D, threads, probs)
+                        : launch_logits<NCH, DT, false>(L, xb, W, bias, T, E, D, threads, probs);
+    if (e != hipSuccess) return e;
+    const int tk = E <= 64 ? 64 : 256;
+    const size_t lds_k = E <= kLdsProbsMax ? (size_t)E * 4 : 0;
+    return launch(Lk, router_topk_kernel, dim3(T), dim3(tk), (uint32_t)lds_k, E, K, norm_topk, probs, routing,
+                  weights);
 }
 
 }  // namespace
 
-hipError_t launch_router(hipStream_t s, int order, int dtype, const float *xb, const void *W, const float *bias, int T,
-                         int E, int D, int K, int norm_topk, float *probs, unsigned *counters, int32_t *routing,
-                         float *weights) {
+hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype, const float *xb, const void *W,
+                         const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,
+                         int32_t *routing, float *weights) {
     if (T <= 0) return hipSuccess;
+    if (T > 65535) return hipErrorInvalidValue;  // grid.y limit of the logits kernel
     if (order == RBT_ORDER_AVX2) {
         return dtype == RBT_DT_BF16
-                   ? launch_t<16, RBT_DT_BF16>(s, xb, W, bias, T, E, D, K, norm_topk, probs, counters, routing, weights)
-                   : launch_t<16, RBT_DT_F32>(s, xb, W, bias, T, E, D, K, norm_topk, probs, counters, routing, weights);
+                   ? launch_t<16, RBT_DT_BF16>(L, Lk, xb, W, bias, T, E, D, K, norm_topk, probs, routing, weights)
+                   : launch_t<16, RBT_DT_F32>(L, Lk, xb, W, bias, T, E, D, K, norm_topk, probs, routing, weights);
     }
     return dtype == RBT_DT_BF16
-               ? launch_t<4, RBT_DT_BF16>(s, xb, W, bias, T, E, D, K, norm_topk, probs, counters, routing, weights)
-               : launch_t<4, RBT_DT_F32>(s, xb, W, bias, T, E, D, K, norm_topk, probs, counters, routing, weights);
+               ? launch_t<4, RBT_DT_BF16>(L, Lk, xb, W, bias, T, E, D, K, norm_topk, probs, routing, weights)
+               : launch_t<4, RBT_DT_F32>(L, Lk, xb, W, bias, T, E, D, K, norm_topk, probs, routing, weights);
 }
 
 }  // namespace rbt

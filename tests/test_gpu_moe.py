@@ -62,6 +62,31 @@ def test_small_shapes(dev, shape, order):
         layer.close()
 
 
+# Shapes whose rows are whole 1 KiB wave-steps take the specialised decode kernels
+# (experts_decode.hip): D, H multiples of 512 (bf16) or 256 (f32).
+FAST_SHAPES = [
+    (512, 8, 2, 512, po.DT_BF16, 1),    # one step per row
+    (1024, 16, 4, 1536, po.DT_BF16, 0),  # 2 steps gate/up, 3 steps down
+    (256, 8, 2, 256, po.DT_F32, 1),
+    (768, 8, 8, 1024, po.DT_F32, 1),     # f32, 4 steps down: slots loaded 4 at a time
+    (2048, 32, 12, 1024, po.DT_BF16, 1),  # K = 12: a full and a partial chunk of 8 slots
+    (4096, 8, 2, 512, po.DT_BF16, 0),    # 8 steps gate/up
+]
+
+
+@pytest.mark.parametrize("shape", FAST_SHAPES, ids=[f"D{s[0]}E{s[1]}K{s[2]}H{s[3]}dt{s[4]}n{s[5]}" for s in FAST_SHAPES])
+def test_fast_path_shapes(dev, shape):
+    D, E, K, H, dt, nt = shape
+    layer = SynthLayer(dev, D, E, K, H, dt, nt, seed=4, w_scale=1.0, fan_in=True)
+    try:
+        for T in (1, 3):
+            xb = layer.make_x(T, seed=21 + T)
+            x = layer.make_x(T, seed=77, bf16=False)
+            check(layer, xb, po.ORDER_AVX2, dev, x=x, label=f"fast D{D}E{E}K{K}H{H}")
+    finally:
+        layer.close()
+
+
 def test_empty_batch(dev):
     layer = SynthLayer(dev, 64, 8, 2, 128, po.DT_BF16, 1, seed=1)
     try:
