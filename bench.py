@@ -34,6 +34,8 @@ D, E, K, H, LAYERS = 2048, 64, 8, 1024, 16
 SEED = 1
 W_SCALE = 0.02
 NX = 64  # distinct input vectors cycled through
+TRAFFIC_KEY = {"gateup": "gateup_fast"}
+KERNEL_DESC = {"gateup": "gateup_fast (softmax + top-k, expert gate+up projections, SwiGLU)"}
 
 
 def hip_events():
@@ -81,6 +83,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-fused", action="store_true", help="separate top-k launch (four launches per layer) "
+                    "instead of the top-k inside the gate/up kernel")
     ap.add_argument("--eager", action="store_true", help="launch every layer from Python instead of replaying a "
                     "captured HIP graph of the steps")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target length of the CPU baseline sample")
@@ -126,6 +130,7 @@ def main():
     routing = dev.malloc(LAYERS * K * 4)
     dev.reserve(layers[0], 1)
     dev.set_router_order(rh.ORDER_AVX2)
+    dev.set_option("fused_decode", 0 if args.no_fused else 1)
 
     def step(s):
         for l in range(LAYERS):
@@ -185,32 +190,25 @@ def main():
     kern = {}
     for name in ("router", "topk", "gateup", "down_combine"):
         tot, n = dev.profile_get(name)
-        kern[name] = {"avg_us": 1000.0 * tot / max(n, 1), "launches": n}
+        if n:
+            kern[name] = {"avg_us": 1000.0 * tot / n, "launches": n}
     dev.profile(False)
 
-    w_gateup = K * 2 * H * D * esz
-    gateup_bytes = w_gateup + D * 4 + K * H * 4  # weights + x read + h written
-    down_bytes = K * D * H * esz + K * H * 4 + D * 4
-    router_bytes = E * D * esz + D * 4
-    topk_bytes = E * 4 * 2 + K * 8  # logits in, probabilities out, routing + weights out
-    layer_alg = E * D * esz + K * 3 * H * D * esz  # 100,925,440: router + 8 experts
-    for name, b in (("router", router_bytes), ("topk", topk_bytes), ("gateup", gateup_bytes),
-                    ("down_combine", down_bytes)):
-        kern[name]["alg_bytes"] = b
-        kern[name]["GBps"] = b / (kern[name]["avg_us"] * 1e-6) / 1e9
-    dom = kern["gateup"]
+    w_experts = K * 3 * H * D * esz  # the 8 selected experts' w1, w3, w2
+    alg_bytes = {
+        "router": E * D * esz + D * 4,
+        "topk": E * 4 * 2 + K * 8,  # logits in, probabilities out, routing + weights out
+        "gateup": K * 2 * H * D * esz + D * 4 + K * H * 4,  # weights + x read + h written
+        "down_combine": K * D * H * esz + K * H * 4 + D * 4,
+    }
+    layer_alg = E * D * esz + w_experts  # 100,925,440: router + 8 experts
+    for name in kern:
+        kern[name]["alg_bytes"] = alg_bytes[name]
+        kern[name]["GBps"] = alg_bytes[name] / (kern[name]["avg_us"] * 1e-6) / 1e9
+    dom_name = "gateup"
+    dom = kern[dom_name]
     layer_us = 1000.0 * ms_per_step / LAYERS
     layer_gbs = layer_alg / (layer_us * 1e-6) / 1e9
-
-    if args.copy_calib_mib:
-        nb = args.copy_calib_mib << 20
-        src, dst = dev.malloc(nb), dev.malloc(nb)
-        dev.memset(src, 1)
-        hipapi.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
-        assert hipapi.hipMemcpyAsync(dst.p, src.p, nb, 3, stream) == 0  # hipMemcpyDeviceToDevice
-        dev.synchronize()
-        dev.free(src)
-        dev.free(dst)
 
     # routing histogram sanity (the last step's selections)
     last_routing = dev.d2h(routing, (LAYERS, K), np.int32)
@@ -222,7 +220,7 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "olmoe_moe_decode_bs1_traffic.json")
     if os.path.exists(tpath):
         try:
-            traffic = json.load(open(tpath))["per_launch"]["gateup_fast"]["bytes"]
+            traffic = json.load(open(tpath))["per_launch"][TRAFFIC_KEY[dom_name]]["bytes"]
         except (KeyError, ValueError):
             traffic = None
 
@@ -250,14 +248,14 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gateup_gemv (expert gate+up projections + SwiGLU)",
+            "kernel": KERNEL_DESC[dom_name],
             "achieved": round(dom["GBps"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": "profiles/olmoe_moe_decode_bs1_traffic.json" if traffic else None,
-            "alg_bytes_per_launch": gateup_bytes,
+            "alg_bytes_per_launch": alg_bytes[dom_name],
             "avg_launch_us": round(dom["avg_us"], 3),
         },
         "layer": {

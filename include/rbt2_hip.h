@@ -61,6 +61,11 @@ void rbt_hip_free(rbt_hip *h);
 /* Last error message of this handle ("" if none); with h == NULL, the last init failure. */
 const char *rbt_hip_last_error(const rbt_hip *h);
 int rbt_hip_set_router_order(rbt_hip *h, int order);
+/* Tuning switch (no counterpart in the reference):
+ *   "fused_decode"  1 (default): a batch-1 block of up to 64 experts runs the softmax + top-k inside
+ *                   the expert gate/up kernel (router logits, gate/up, down: three launches);
+ *                   0: a separate top-k launch (four launches). Results are identical. */
+int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
 
 /* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the
  * header exactly like load_model() (rabbit2.c:199-228) and keeps every expert resident, which

@@ -59,6 +59,7 @@ struct rbt_hip {
     std::vector<LayerOff> layers;
     Workspace ws;
     Profile prof;
+    int fused_decode = 1;  // option "fused_decode": batch-1 top-k inside the gate/up kernel
     // staging for the host-pointer entry points
     void *stage = nullptr;
     uint64_t stage_bytes = 0;
@@ -328,14 +329,24 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
     Workspace &w = h->ws;
     int32_t *routing = routing_dev ? routing_dev : w.routing;
     float *weights = weights_dev ? weights_dev : w.weights;
+    const bool decode_kernels = experts_decode_supported(L->dtype, T, L->top_k, L->dim, L->expert_hidden, L->experts,
+                                                         L->expert_stride, xb_dev, w.hbuf);
+    if (decode_kernels && h->fused_decode && T == 1 && L->n_experts <= kTopkInGateupMaxE) {
+        // batch 1: router logits, then gate/up (with the top-k in every block), then down + combine
+        HIP_OK(h, launch_router_logits(lc(h, kProfRouter), h->order, L->dtype, xb_dev, L->router, L->router_bias, T,
+                                       L->n_experts, L->dim, w.probs));
+        HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
+                                        routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
+                                        moe_dev, w.probs, L->n_experts, L->norm_topk));
+        return prof_collect(h);
+    }
     HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
                             L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
                             weights));
-    if (experts_decode_supported(L->dtype, T, L->top_k, L->dim, L->expert_hidden, L->experts, L->expert_stride, xb_dev,
-                                 w.hbuf)) {
+    if (decode_kernels) {
         HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
                                         routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
-                                        moe_dev));
+                                        moe_dev, nullptr, L->n_experts, L->norm_topk));
     } else {
         HIP_OK(h, launch_gateup_gemv(lc(h, kProfGateup), L->dtype, L->experts, L->expert_stride, routing, xb_dev, T,
                                      L->top_k, L->dim, L->expert_hidden, w.hbuf));
@@ -456,6 +467,16 @@ int rbt_hip_synchronize(rbt_hip *h) {
     if (!h) return fail(nullptr, "synchronize: handle is NULL");
     if (!set_device(h)) return 0;
     HIP_OK(h, hipStreamSynchronize(h->stream));
+    return 1;
+}
+
+int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
+    if (!h || !name) return fail(h, "set_option: NULL argument");
+    if (strcmp(name, "fused_decode") == 0) {
+        h->fused_decode = value != 0;
+    } else {
+        return fail(h, "set_option: unknown option '%s'", name);
+    }
     return 1;
 }
 

@@ -20,6 +20,73 @@
 namespace rbt {
 namespace {
 
+constexpr int KMAX_T = 64;  // selected experts per token (the engine's MAX_TOPK, rabbit2.c:59)
+constexpr int EMAX_T = 64;  // experts per layer for the in-kernel top-k (one per lane of wave 0)
+
+// Softmax + top-k of one token's logits, the engine's arithmetic (rabbit2.c:399-405, :516-528,
+// :539): leaves the expert ids in s_idx[0..K) and the combine weights in s_w[0..K). Called by every
+// thread of the block (it ends with a barrier); wave 0 does the work, exchanging values through
+// LDS with wave-scope fences only (a wave's LDS operations execute in order).
+__device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+__device__ void block_topk(const float *__restrict__ logits, int E, int K, int norm_topk, float *s_v, int *s_idx,
+                           float *s_pw, float *s_w, float *s_sum) {
+    (void)s_sum;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    if (tid < kWave) {
+        const float v = lane < E ? logits[lane] : -INFINITY;
+        float mx = wave_max(v);  // ignores NaN like the engine's '>' scan ...
+        const float first = lane_value(v, 0);
+        if (first != first) mx = first;  // ... which starts from element 0
+        const float e = lane < E ? (float)exp((double)(v - mx)) : 0.0f;
+        s_v[lane] = e;
+        wave_lds_sync();
+        // every lane forms the sum itself, sequentially in the engine's order (entries past E are 0
+        // and come last, so they do not change it)
+        const f32x4 *p4 = reinterpret_cast<const f32x4 *>(s_v);
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < EMAX_T / 4; ++q) {
+            const f32x4 v4 = p4[q];
+            sum = sum + v4.x;
+            sum = sum + v4.y;
+            sum = sum + v4.z;
+            sum = sum + v4.w;
+        }
+        const float p = e / sum;
+        wave_lds_sync();
+        s_v[lane] = p;
+        wave_lds_sync();
+        int rank;
+        if (sum != sum) {
+            rank = lane;  // all NaN: the engine keeps the first unused index each round
+        } else {
+            // four independent counters keep the dependent-add chain short (entries past E are 0
+            // and never beat a probability of a real expert; lanes past E are not stored)
+            int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+#pragma unroll
+            for (int q = 0; q < EMAX_T / 4; ++q) {
+                const f32x4 v4 = p4[q];
+                const int j = 4 * q;
+                r0 += (v4.x > p) | ((v4.x == p) & (j < lane));
+                r1 += (v4.y > p) | ((v4.y == p) & (j + 1 < lane));
+                r2 += (v4.z > p) | ((v4.z == p) & (j + 2 < lane));
+                r3 += (v4.w > p) | ((v4.w == p) & (j + 3 < lane));
+            }
+            rank = (r0 + r1) + (r2 + r3);
+        }
+        if (lane < E && rank < K) {
+            s_idx[rank] = lane;
+            s_pw[rank] = p;
+        }
+        wave_lds_sync();
+        float wsum = 0.0f;
+        for (int k = 0; k < K; ++k) wsum = wsum + s_pw[k];
+        if (lane < K) s_w[lane] = norm_topk ? s_pw[lane] / wsum : s_pw[lane];
+    }
+    __syncthreads();
+}
+
 template <int DT>
 struct Elem {
     static constexpr int kEsz = DT == RBT_DT_F32 ? 4 : 2;
@@ -54,20 +121,39 @@ __device__ __forceinline__ float dot16r(const u32x4 w, const f32x4 x0, const f32
 }
 
 // grid: ceil(P*H/JW / 4) blocks of 4 waves; requires H % JW == 0 and D == NC * 64 * kPer.
-template <int DT, int NC, int JW>
+// TOPK (batch 1 only): every block first runs the token's softmax + top-k from the router logits
+// (`logits`, E experts) instead of reading `routing`; block 0 publishes routing/weights for the
+// down kernel. Saves a launch on the decode critical path.
+template <int DT, int NC, int JW, bool TOPK>
 __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
-                                                          const int32_t *__restrict__ routing,
+                                                          int32_t *__restrict__ routing,
                                                           const float *__restrict__ xb, int K, int H,
-                                                          long long items, float *__restrict__ hbuf) {
+                                                          long long items, float *__restrict__ hbuf,
+                                                          const float *__restrict__ logits, int E, int norm_topk,
+                                                          float *__restrict__ weights) {
     constexpr int kEsz = Elem<DT>::kEsz, kPer = Elem<DT>::kPer;
     constexpr int D = NC * kWave * kPer;
     const int lane = threadIdx.x & (kWave - 1);
     const long long item = (long long)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
-    if (item >= items) return;
+    int e;
+    if constexpr (TOPK) {
+        __shared__ __align__(16) float s_v[EMAX_T];
+        __shared__ int s_idx[KMAX_T];
+        __shared__ float s_pw[KMAX_T], s_w[KMAX_T], s_sum;
+        block_topk(logits, E, K, norm_topk, s_v, s_idx, s_pw, s_w, &s_sum);
+        if (blockIdx.x == 0 && (int)threadIdx.x < K) {
+            routing[threadIdx.x] = s_idx[threadIdx.x];
+            weights[threadIdx.x] = s_w[threadIdx.x];
+        }
+        if (item >= items) return;
+        e = s_idx[(int)((item * JW) / H)];
+    } else {
+        if (item >= items) return;
+        e = routing[(item * JW) / H];
+    }
     const long long row0 = item * JW;
     const long long p = row0 / H;
     const int j0 = (int)(row0 - p * H);
-    const int e = routing[p];
     const int t = (int)(p / K);
     const uint8_t *w1 = experts + (size_t)e * stride + (size_t)j0 * D * kEsz;
     const uint8_t *w3 = w1 + (size_t)H * D * kEsz;
@@ -220,12 +306,16 @@ __global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restric
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int DT, int NC>
-hipError_t gateup_nc(const Launch &L, const uint8_t *E, uint64_t stride, const int32_t *routing, const float *xb,
-                     int T, int K, int H, float *hbuf) {
+hipError_t gateup_nc(const Launch &L, const uint8_t *E, uint64_t stride, int32_t *routing, const float *xb, int T,
+                     int K, int H, float *hbuf, const float *logits, int nE, int norm_topk, float *weights) {
     constexpr int JW = 2;
     const long long items = (long long)T * K * H / JW;
-    return launch(L, gateup_fast_kernel<DT, NC, JW>, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, E, stride,
-                  routing, xb, K, H, items, hbuf);
+    const dim3 g((unsigned)((items + 3) / 4)), b(256);
+    if (logits)
+        return launch(L, gateup_fast_kernel<DT, NC, JW, true>, g, b, 0, E, stride, routing, xb, K, H, items, hbuf,
+                      logits, nE, norm_topk, weights);
+    return launch(L, gateup_fast_kernel<DT, NC, JW, false>, g, b, 0, E, stride, routing, xb, K, H, items, hbuf,
+                  logits, nE, norm_topk, weights);
 }
 
 template <int DT, int NH>
@@ -239,19 +329,19 @@ hipError_t down_nh(const Launch &L, const uint8_t *E, uint64_t stride, const int
 }
 
 template <int DT>
-hipError_t decode_dt(const Launch &Lg, const Launch &Ld, const uint8_t *E, uint64_t stride, const int32_t *routing,
-                     const float *weights, const float *xb, float *hbuf, int T, int K, int D, int H, float *x_inout,
-                     float *moe_out) {
+hipError_t decode_dt(const Launch &Lg, const Launch &Ld, const uint8_t *E, uint64_t stride, int32_t *routing,
+                     float *weights, const float *xb, float *hbuf, int T, int K, int D, int H, float *x_inout,
+                     float *moe_out, const float *logits, int nE, int norm_topk) {
     constexpr int step = kWave * Elem<DT>::kPer;
     const int nc = D / step, nh = H / step;
     hipError_t e;
     switch (nc) {
-        case 1: e = gateup_nc<DT, 1>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
-        case 2: e = gateup_nc<DT, 2>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
-        case 3: e = gateup_nc<DT, 3>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
-        case 4: e = gateup_nc<DT, 4>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
-        case 6: e = gateup_nc<DT, 6>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
-        case 8: e = gateup_nc<DT, 8>(Lg, E, stride, routing, xb, T, K, H, hbuf); break;
+        case 1: e = gateup_nc<DT, 1>(Lg, E, stride, routing, xb, T, K, H, hbuf, logits, nE, norm_topk, weights); break;
+        case 2: e = gateup_nc<DT, 2>(Lg, E, stride, routing, xb, T, K, H, hbuf, logits, nE, norm_topk, weights); break;
+        case 3: e = gateup_nc<DT, 3>(Lg, E, stride, routing, xb, T, K, H, hbuf, logits, nE, norm_topk, weights); break;
+        case 4: e = gateup_nc<DT, 4>(Lg, E, stride, routing, xb, T, K, H, hbuf, logits, nE, norm_topk, weights); break;
+        case 6: e = gateup_nc<DT, 6>(Lg, E, stride, routing, xb, T, K, H, hbuf, logits, nE, norm_topk, weights); break;
+        case 8: e = gateup_nc<DT, 8>(Lg, E, stride, routing, xb, T, K, H, hbuf, logits, nE, norm_topk, weights); break;
         default: return hipErrorNotSupported;
     }
     if (e != hipSuccess) return e;
@@ -277,12 +367,14 @@ bool experts_decode_supported(int dtype, int T, int K, int D, int H, const void 
 }
 
 hipError_t launch_experts_decode(const Launch &Lg, const Launch &Ld, int dtype, const void *experts, uint64_t stride,
-                                 const int32_t *routing, const float *weights, const float *xb, float *hbuf, int T,
-                                 int K, int D, int H, float *x_inout, float *moe_out) {
-    const uint8_t *E = static_cast<const uint8_t *>(experts);
-    return dtype == RBT_DT_BF16
-               ? decode_dt<RBT_DT_BF16>(Lg, Ld, E, stride, routing, weights, xb, hbuf, T, K, D, H, x_inout, moe_out)
-               : decode_dt<RBT_DT_F32>(Lg, Ld, E, stride, routing, weights, xb, hbuf, T, K, D, H, x_inout, moe_out);
+                                 int32_t *routing, float *weights, const float *xb, float *hbuf, int T, int K, int D,
+                                 int H, float *x_inout, float *moe_out, const float *logits, int E, int norm_topk) {
+    if (logits && (T != 1 || E > EMAX_T)) return hipErrorInvalidValue;
+    const uint8_t *Eb = static_cast<const uint8_t *>(experts);
+    return dtype == RBT_DT_BF16 ? decode_dt<RBT_DT_BF16>(Lg, Ld, Eb, stride, routing, weights, xb, hbuf, T, K, D, H,
+                                                         x_inout, moe_out, logits, E, norm_topk)
+                                : decode_dt<RBT_DT_F32>(Lg, Ld, Eb, stride, routing, weights, xb, hbuf, T, K, D, H,
+                                                        x_inout, moe_out, logits, E, norm_topk);
 }
 
 }  // namespace rbt

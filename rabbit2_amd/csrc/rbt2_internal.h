@@ -37,10 +37,43 @@ __device__ __forceinline__ f32x4 ld_stream_f4(const void *p) {
 }
 __device__ __forceinline__ f32x4 ld_f4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// Cross-lane moves through DPP (a VALU operand modifier, no LDS round trip). Within each row of 16
+// lanes: swap neighbours, swap pairs, mirror each half-row, mirror the row -- after four steps every
+// lane of a row holds the same row total (each step adds commutative partners, so all lanes of a
+// row see identical operands). ds_bpermute-based shuffles cost an LDS round trip per step instead.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    v += dpp_f<kDppMirror>(v);
     return v;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes, returned to every lane (row totals combined in a fixed order).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row_sum16(v);
+    return ((lane_value(v, 0) + lane_value(v, 16)) + lane_value(v, 32)) + lane_value(v, 48);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // Where and how a kernel is launched: the stream, and optionally a pair of events that the runtime
@@ -65,6 +98,10 @@ hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype
                          const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,
                          int32_t *routing, float *weights);
 
+// Only the logits kernel of launch_router.
+hipError_t launch_router_logits(const Launch &L, int order, int dtype, const float *xb, const void *W,
+                                const float *bias, int T, int E, int D, float *logits);
+
 // Per-(token, slot) GEMV form of the expert FFN (decode and small batches).
 hipError_t launch_gateup_gemv(const Launch &L, int dtype, const void *experts, uint64_t stride, const int32_t *routing,
                               const float *xb, int T, int K, int D, int H, float *hbuf);
@@ -78,8 +115,11 @@ hipError_t launch_down_combine(const Launch &L, int dtype, const void *experts, 
 bool experts_decode_supported(int dtype, int T, int K, int D, int H, const void *experts, uint64_t stride,
                               const float *xb, const float *hbuf);
 hipError_t launch_experts_decode(const Launch &Lg, const Launch &Ld, int dtype, const void *experts, uint64_t stride,
-                                 const int32_t *routing, const float *weights, const float *xb, float *hbuf, int T,
-                                 int K, int D, int H, float *x_inout, float *moe_out);
+                                 int32_t *routing, float *weights, const float *xb, float *hbuf, int T, int K, int D,
+                                 int H, float *x_inout, float *moe_out, const float *logits, int E, int norm_topk);
+// With logits != NULL (batch 1, E <= 64) the gate/up kernel runs the softmax + top-k itself and
+// fills routing/weights; otherwise it reads routing written by the top-k kernel.
+constexpr int kTopkInGateupMaxE = 64;
 
 // Dense matvec (one row per wave).
 hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);

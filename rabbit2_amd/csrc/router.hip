@@ -53,8 +53,7 @@ __device__ __forceinline__ float widen(typename RouterTile<DT, false>::W w) {
 }
 
 __device__ float block_max_f(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    v = wave_max(v);
     const int nw = blockDim.x / kWave;
     if (nw == 1) return v;
     const int w = threadIdx.x / kWave;
@@ -326,6 +325,22 @@ hipError_t launch_t(const Launch &L, const Launch &Lk, const float *xb, const vo
 }
 
 }  // namespace
+
+hipError_t launch_router_logits(const Launch &L, int order, int dtype, const float *xb, const void *W,
+                                const float *bias, int T, int E, int D, float *logits) {
+    if (T <= 0) return hipSuccess;
+    if (T > 65535) return hipErrorInvalidValue;
+    if (order == RBT_ORDER_AVX2) {
+        const int threads = T > 8 ? 256 : 64;
+        if (dtype == RBT_DT_BF16)
+            return threads == 64 ? launch_logits<16, RBT_DT_BF16, true>(L, xb, W, bias, T, E, D, 64, logits)
+                                 : launch_logits<16, RBT_DT_BF16, false>(L, xb, W, bias, T, E, D, 256, logits);
+        return threads == 64 ? launch_logits<16, RBT_DT_F32, true>(L, xb, W, bias, T, E, D, 64, logits)
+                             : launch_logits<16, RBT_DT_F32, false>(L, xb, W, bias, T, E, D, 256, logits);
+    }
+    return dtype == RBT_DT_BF16 ? launch_logits<4, RBT_DT_BF16, false>(L, xb, W, bias, T, E, D, 64, logits)
+                                : launch_logits<4, RBT_DT_F32, false>(L, xb, W, bias, T, E, D, 64, logits);
+}
 
 hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype, const float *xb, const void *W,
                          const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,

@@ -20,7 +20,7 @@ EXPORTS = (
     "rbt_hip_layer", "rbt_hip_moe", "rbt_hip_moe_dev", "rbt_hip_reserve", "rbt_hip_expert_counts_dev",
     "rbt_hip_matvec", "rbt_hip_matvec_dev", "rbt_hip_malloc", "rbt_hip_free_dev", "rbt_hip_h2d", "rbt_hip_d2h",
     "rbt_hip_memset_dev", "rbt_hip_synchronize", "rbt_hip_stream", "rbt_hip_fill_normal", "rbt_hip_profile_enable",
-    "rbt_hip_profile_get",
+    "rbt_hip_profile_get", "rbt_hip_set_option",
 )
 
 
@@ -73,6 +73,7 @@ def lib():
         L.rbt_hip_stream.argtypes, L.rbt_hip_stream.restype = [vp], vp
         L.rbt_hip_fill_normal.argtypes = [vp, vp, i32, u64, u64, u64, u64, f32, f32]
         L.rbt_hip_profile_enable.argtypes = [vp, i32]
+        L.rbt_hip_set_option.argtypes = [vp, C.c_char_p, C.c_int64]
         L.rbt_hip_profile_get.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]
         _lib = L
     return _lib
@@ -131,6 +132,9 @@ class Device:
 
     def set_router_order(self, order):
         self._check(self.L.rbt_hip_set_router_order(self.h, order))
+
+    def set_option(self, name, value):
+        self._check(self.L.rbt_hip_set_option(self.h, name.encode(), int(value)))
 
     # ---- memory
     def malloc(self, nbytes):

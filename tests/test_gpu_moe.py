@@ -111,6 +111,24 @@ def test_olmoe_decode(dev, olmoe_layer, order):
         check(olmoe_layer, xb, order, dev, label=f"olmoe decode seed {s}")
 
 
+def test_olmoe_decode_fused_and_four_launch_paths(dev, olmoe_layer):
+    """Batch-1 decode runs the top-k inside the gate/up kernel by default (three launches); the
+    four-launch form has a separate top-k kernel. Both meet the bar, on the same routing."""
+    dev.set_router_order(po.ORDER_AVX2)
+    try:
+        for s in range(3):
+            xb = olmoe_layer.make_x(1, seed=40 + s)
+            x = olmoe_layer.make_x(1, seed=60 + s, bf16=False)
+            dev.set_option("fused_decode", 1)
+            got_f, want = check(olmoe_layer, xb, po.ORDER_AVX2, dev, x=x, label=f"fused seed {s}")
+            dev.set_option("fused_decode", 0)
+            got_u, _ = check(olmoe_layer, xb, po.ORDER_AVX2, dev, x=x, label=f"four-launch seed {s}")
+            assert np.array_equal(got_f["routing"], got_u["routing"])
+            assert np.array_equal(got_f["weights"], got_u["weights"])
+    finally:
+        dev.set_option("fused_decode", 1)
+
+
 def test_olmoe_decode_deterministic(dev, olmoe_layer):
     dev.set_router_order(po.ORDER_AVX2)
     xb = olmoe_layer.make_x(1, seed=7)
