@@ -25,8 +25,8 @@ struct LayerOff {
     uint64_t attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, router, experts;
 };
 
-enum ProfKernel { kProfRouter, kProfTopk, kProfGateup, kProfDown, kProfCount };
-const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_combine"};
+enum ProfKernel { kProfRouter, kProfTopk, kProfGateup, kProfDown, kProfDispatch, kProfCombine, kProfCount };
+const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_combine", "dispatch", "combine"};
 
 struct Profile {
     bool on = false;
@@ -42,6 +42,8 @@ struct Workspace {
     int32_t *routing = nullptr;   // [T][K]
     float *weights = nullptr;     // [T][K]
     float *hbuf = nullptr;        // [T*K][H]
+    uint8_t *pre = nullptr;       // grouped-path lists and down outputs (prefill_workspace_bytes)
+    size_t pre_bytes = 0;
 };
 
 }  // namespace
@@ -60,6 +62,8 @@ struct rbt_hip {
     Workspace ws;
     Profile prof;
     int fused_decode = 1;  // option "fused_decode": batch-1 top-k inside the gate/up kernel
+    int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
+    const int32_t *expert_counts = nullptr;  // histogram of the last grouped-path call
     // staging for the host-pointer entry points
     void *stage = nullptr;
     uint64_t stage_bytes = 0;
@@ -152,6 +156,7 @@ void ws_release(Workspace &w) {
     (void)hipFree(w.routing);
     (void)hipFree(w.weights);
     (void)hipFree(w.hbuf);
+    (void)hipFree(w.pre);
     w = Workspace{};
 }
 
@@ -163,6 +168,7 @@ int ws_reserve(rbt_hip *h, int T, int E, int K, int H) {
               nH = H > w.H ? H : w.H;
     HIP_OK(h, hipStreamSynchronize(h->stream));
     ws_release(w);
+    h->expert_counts = nullptr;
     HIP_OK(h, hipMalloc(&w.probs, sizeof(float) * (size_t)nT * nE));
     HIP_OK(h, hipMalloc(&w.routing, sizeof(int32_t) * (size_t)nT * nK));
     HIP_OK(h, hipMalloc(&w.weights, sizeof(float) * (size_t)nT * nK));
@@ -171,6 +177,20 @@ int ws_reserve(rbt_hip *h, int T, int E, int K, int H) {
     w.E = nE;
     w.K = nK;
     w.H = nH;
+    return 1;
+}
+
+// Grows the grouped-path workspace (never shrinks).
+int pre_reserve(rbt_hip *h, size_t bytes) {
+    Workspace &w = h->ws;
+    if (bytes <= w.pre_bytes) return 1;
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    (void)hipFree(w.pre);
+    w.pre = nullptr;
+    w.pre_bytes = 0;
+    h->expert_counts = nullptr;
+    HIP_OK(h, hipMalloc(&w.pre, bytes));
+    w.pre_bytes = bytes;
     return 1;
 }
 
@@ -314,7 +334,11 @@ int rbt_hip_reserve(rbt_hip *h, const rbt_moe_layer *L, int max_tokens) {
     if (!h) return fail(nullptr, "reserve: handle is NULL");
     if (!check_layer(h, L) || !set_device(h)) return 0;
     if (max_tokens < 0) return fail(h, "reserve: negative token count");
-    return ws_reserve(h, max_tokens > 0 ? max_tokens : 1, L->n_experts, L->top_k, L->expert_hidden);
+    const int T = max_tokens > 0 ? max_tokens : 1;
+    if (!ws_reserve(h, T, L->n_experts, L->top_k, L->expert_hidden)) return 0;
+    if (T >= h->prefill_min_tokens)
+        return pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim));
+    return 1;
 }
 
 int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, float *x_dev, float *moe_dev,
@@ -343,7 +367,15 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
     HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
                             L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
                             weights));
-    if (decode_kernels) {
+    if (prefill_supported(L->dtype, T, h->prefill_min_tokens, L->n_experts, L->top_k, L->dim, L->expert_hidden,
+                          L->experts, L->expert_stride, xb_dev)) {
+        if (!pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim))) return 0;
+        int32_t *counts = nullptr;
+        HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
+                                 L->experts, L->expert_stride, xb_dev, T, L->n_experts, L->top_k, L->dim,
+                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts));
+        h->expert_counts = counts;
+    } else if (decode_kernels) {
         HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
                                         routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
                                         moe_dev, nullptr, L->n_experts, L->norm_topk));
@@ -356,10 +388,7 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
     return prof_collect(h);
 }
 
-const int32_t *rbt_hip_expert_counts_dev(rbt_hip *h) {
-    (void)h;
-    return nullptr;
-}
+const int32_t *rbt_hip_expert_counts_dev(rbt_hip *h) { return h ? h->expert_counts : nullptr; }
 
 int rbt_hip_moe(rbt_hip *h, int layer, const float *xb, int T, float *x_inout, int32_t *routing_out) {
     if (!h) return fail(nullptr, "moe: handle is NULL");
@@ -474,6 +503,9 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
     if (!h || !name) return fail(h, "set_option: NULL argument");
     if (strcmp(name, "fused_decode") == 0) {
         h->fused_decode = value != 0;
+    } else if (strcmp(name, "prefill_min_tokens") == 0) {
+        if (value < 1 || value > 65536) return fail(h, "set_option: prefill_min_tokens must be in [1, 65536]");
+        h->prefill_min_tokens = (int)value;
     } else {
         return fail(h, "set_option: unknown option '%s'", name);
     }

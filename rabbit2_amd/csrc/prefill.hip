@@ -1,0 +1,421 @@
+// Prefill (many tokens per call): expert dispatch, grouped SwiGLU GEMMs on bf16 MFMA, combine.
+//
+// Reference semantics: rabbit2/src/rabbit2.c:531-542, applied to every token of the batch (the
+// engine evaluates a prompt one token at a time, :703-714; the tokens are independent inside the
+// MoE block): for each selected expert k of a token, h = silu(W1 xb) * (W3 xb), tmp = W2 h,
+// moe += w_k * tmp in selection order, x += moe. Expert blob layout w1[H][D] | w3[H][D] | w2[D][H]
+// (rabbit2.c:173, rabbit2/tools/rbt2.py:152-156), bf16 elements.
+//
+// 1. dispatch_kernel: per-expert lists of the (token, slot) pairs, stable in pair order (counts,
+//    row offsets, perm, inverse perm) and the per-expert count of 64-row tiles.
+// 2. grouped_mfma_kernel<2, ...>: for each expert's rows, h = silu(W1 a) * (W3 a) (f32 rows).
+//    grouped_mfma_kernel<1, ...>: y = W2 h (f32 rows). Both on v_mfma_f32_16x16x32_bf16.
+//    The f32 activations are split into bf16 hi + lo parts and both parts are multiplied (two MFMAs
+//    per product). The bf16 weights are exact, so each product keeps ~16 bits of the activation
+//    instead of 8. A full 64-row tile then does 64 rows x 2 parts x 2 flop = 256 flop per weight
+//    element, 128 flop per weight byte: below the bf16 MFMA/HBM ridge (2.5 PFLOP/s / 8 TB/s =
+//    312), so the kernels stay bound by HBM.
+//    Tiles: 64 rows x 64*NB columns per block of 4 waves; K in chunks of KC staged through LDS
+//    (double-buffered); the weight operand streams from HBM into registers one chunk ahead.
+//    Tile order (expert, column tile, row tile), split into 8 contiguous ranges, one per XCD (the
+//    hardware hands block b to XCD b % 8): the row tiles of a hot expert then share each weight
+//    tile in that XCD's L2, and an expert's activation rows are reused across its column tiles.
+// 3. combine_rows_kernel: moe[t] = sum_k w[t][k] * y[pos(t,k)] in selection order, x += moe.
+#include <math.h>
+
+#include <algorithm>
+
+#include "rbt2_internal.h"
+
+namespace rbt {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kMT = 64;  // rows (pairs) per tile
+constexpr int kDispatchMaxE = 256;
+
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// ---------------------------------------------------------------- dispatch (one block, 1024 threads)
+// routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);
+// perm[P]: pair ids grouped by expert, increasing within an expert; pos_of[P]: inverse of perm;
+// m_off[E+1]: exclusive prefix of ceil(counts / 64).
+__global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ routing, int P, int E,
+                                                        int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                                                        int32_t *__restrict__ perm, int32_t *__restrict__ pos_of,
+                                                        int32_t *__restrict__ m_off) {
+    __shared__ int s_cnt[kDispatchMaxE];
+    __shared__ int s_off[kDispatchMaxE];
+    __shared__ int s_run[kDispatchMaxE];
+    __shared__ int s_w[16][kDispatchMaxE];  // per-wave counts of the current chunk
+    __shared__ int s_scan[1024];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int e = tid; e < E; e += 1024) {
+        s_cnt[e] = 0;
+        s_run[e] = 0;
+    }
+    __syncthreads();
+    for (int p = tid; p < P; p += 1024) {
+        const int r = routing[p];
+        atomicAdd(&s_cnt[min(max(r, 0), E - 1)], 1);
+    }
+    __syncthreads();
+    // exclusive scans of the counts (pass 0) and of the tile counts (pass 1), Hillis-Steele
+    for (int pass = 0; pass < 2; ++pass) {
+        int v = 0;
+        if (tid < E) v = pass == 0 ? s_cnt[tid] : (s_cnt[tid] + kMT - 1) / kMT;
+        s_scan[tid] = v;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            const int add = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += add;
+            __syncthreads();
+        }
+        const int incl = s_scan[tid];
+        int32_t *dst = pass == 0 ? offsets : m_off;
+        if (tid < E) {
+            dst[tid] = incl - v;
+            if (pass == 0) {
+                s_off[tid] = incl - v;
+                counts[tid] = v;
+            }
+        }
+        if (tid == E - 1) dst[E] = incl;
+        __syncthreads();
+    }
+    // stable placement, 1024 pairs at a time; rank within the wave from ballots over the expert bits
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    for (int c0 = 0; c0 < P; c0 += 1024) {
+        for (int i = tid; i < 16 * kDispatchMaxE; i += 1024) (&s_w[0][0])[i] = 0;
+        __syncthreads();
+        const int p = c0 + tid;
+        const bool valid = p < P;
+        const int e = valid ? min(max(routing[p], 0), E - 1) : 0;
+        uint64_t same = __ballot(valid);
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (e >> b) & 1;
+            const uint64_t ones = __ballot(bit);
+            same &= bit ? ones : ~ones;
+        }
+        const int before = __popcll(same & below);
+        if (valid && (same >> lane) == 1ull) s_w[wv][e] = before + 1;  // last lane of its expert
+        __syncthreads();
+        int pos = 0;
+        if (valid) {
+            pos = s_off[e] + s_run[e] + before;
+            for (int w = 0; w < wv; ++w) pos += s_w[w][e];
+        }
+        __syncthreads();
+        if (tid < E) {
+            int tot = 0;
+            for (int w = 0; w < 16; ++w) tot += s_w[w][tid];
+            s_run[tid] += tot;
+        }
+        if (valid) {
+            perm[pos] = p;
+            pos_of[p] = pos;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- activation split
+// x (f32) -> hi = bf16_rne(x), lo = bf16_rne(x - hi): hi + lo carries ~16 significant bits, and every
+// MFMA product with an exact bf16 weight is exact in the f32 accumulator.
+__global__ __launch_bounds__(256) void split_hilo_kernel(const float *__restrict__ x, size_t n8,
+                                                        uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
+        const f32x4 a = ld_f4(x + 8 * i), b = ld_f4(x + 8 * i + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            h[k] = f32_to_bf16_rne(v[k]);
+            l[k] = f32_to_bf16_rne(v[k] - __uint_as_float(h[k] << 16));
+        }
+        *reinterpret_cast<u32x4 *>(hi + 8 * i) = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                                                      h[6] | (h[7] << 16)};
+        *reinterpret_cast<u32x4 *>(lo + 8 * i) = u32x4{l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16),
+                                                      l[6] | (l[7] << 16)};
+    }
+}
+
+// ---------------------------------------------------------------- grouped GEMM
+// Direct HBM -> LDS copies (global_load_lds_dwordx4): each lane's 16 bytes land at LDS m0 + 16*lane, so
+// one instruction fills 1 KiB of LDS in lane order and costs no registers. They are issued from inline
+// assembly and waited for by hand (s_waitcnt vmcnt): the compiler, which would otherwise wait for every
+// pending copy before any LDS read, does not see them. The main loop issues no other vector-memory
+// operation, so vmcnt counts exactly these copies.
+__device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds_byte) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_byte), "v"(g) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Tile: 64 list rows x 256 weight rows (gate/up: 128 of W1 and the same 128 of W3; down: 256 of W2),
+// reduction in chunks of 64 (128 bytes of each bf16 row). A chunk is one ring stage in LDS:
+//   weights  256 rows x 128 B   (32 KiB)
+//   act hi    64 rows x 128 B   ( 8 KiB)   bf16 hi plane of the 64 activation rows
+//   act lo    64 rows x 128 B   ( 8 KiB)
+// Three stages (144 KiB): while the MFMAs run on stage c, the copies of stages c+1 and c+2 are in flight.
+// Inside a stage, row r's 16-byte granule g sits at slot g ^ ((r >> 1) & 7) of the row: the MFMA
+// operand reads (16 consecutive rows at one granule per 16 lanes) then hit 16 distinct bank groups.
+// Copies: per stage 32 weight + 16 activation instructions of 8 rows x 128 B, 6 per wave.
+constexpr int kGRows = kMT, kGWRows = 256, kGKC = 64, kGStages = 3;
+constexpr int kGWBytes = kGWRows * 128, kGABytes = kGRows * 128;
+constexpr int kGStageBytes = kGWBytes + 2 * kGABytes;  // 48 KiB
+constexpr int kGDmaPerWave = 6;
+
+__device__ __forceinline__ int swz(int r, int g) { return g ^ ((r >> 1) & 7); }
+
+// MATS = 2: h = silu(W1 a) * (W3 a) for a = xb rows gathered through perm (N = H columns, Kd = D),
+//           written as bf16 hi/lo planes [P][N] (the next GEMM's activation operand).
+// MATS = 1: y = W2 a for a = the h planes in list order (N = D, Kd = H), written as f32 [P][N].
+// Waves: w = 4*ch + rg computes list rows [16 rg, +16) x the ch-th half of the tile's weight rows
+// (8 blocks of 16: gate/up W1 blocks 4ch..4ch+3 and the matching W3 blocks; down W2 blocks 8ch..8ch+7).
+// Requirements (prefill_supported): N % (256 / MATS) == 0, Kd % 64 == 0, 16-byte aligned rows.
+template <int MATS>
+__global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
+    const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
+    int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
+    uint16_t *__restrict__ out_lo) {
+    constexpr int NTILE = kGWRows / MATS;  // output columns per tile
+    __shared__ __align__(1024) uint8_t ring[kGStages * kGStageBytes];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, rg = w & 3, ch = w >> 2;
+    const int ntiles_n = N / NTILE;
+    const int total = m_off[E] * ntiles_n;
+    const int range = (total + 7) >> 3;
+    const int slot = (int)(blockIdx.x >> 3);
+    const int tau = (int)(blockIdx.x & 7) * range + slot;
+    if (slot >= range || tau >= total) return;
+    int lo = 0, hi = E - 1;  // the expert owning tile tau: the last e with m_off[e] * ntiles_n <= tau
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (m_off[mid] * ntiles_n <= tau)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const int e = lo;
+    const int me = m_off[e + 1] - m_off[e];
+    const int local = tau - m_off[e] * ntiles_n;
+    const int jt = local / me, il = local - jt * me;
+    const int row0 = offsets[e] + il * kGRows;
+    const int rows = min(kGRows, counts[e] - il * kGRows);
+    const int n0 = jt * NTILE;
+    const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
+
+    // copy sources of this lane (one pointer per instruction; each stage adds 128 bytes)
+    const uint8_t *wsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 4 * w + i, r = 8 * t + (lane >> 3), g = swz(r, lane & 7);
+        const uint8_t *base = experts + (size_t)e * stride + w_off;
+        int wr = n0 + r;
+        if constexpr (MATS == 2) {
+            if (r >= 128) {
+                base = experts + (size_t)e * stride + w3_off;
+                wr = n0 + r - 128;
+            }
+        }
+        wsrc[i] = base + (size_t)wr * rowb + 16 * g;
+    }
+    const uint8_t *asrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int u = 2 * w + i, plane = u >> 3, r = 8 * (u & 7) + (lane >> 3), g = swz(r, lane & 7);
+        const int lr = row0 + (r < rows ? r : 0);  // rows past the list re-read its first row
+        const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
+        asrc[i] = reinterpret_cast<const uint8_t *>(plane ? a_lo : a_hi) + arow * rowb + 16 * g;
+    }
+    const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
+    auto issue = [&](int c) {
+        const uint32_t sb = ring0 + (uint32_t)((c % kGStages) * kGStageBytes);
+        const size_t kb = (size_t)c * 128;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (4 * w + i) * 1024));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + kGWBytes + (2 * w + i) * 1024));
+    };
+
+    // MFMA operand reads: lane -> row (lane % 16) of a 16-row block, logical granule 4*ks + lane / 16
+    int brow[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        int blk;
+        if constexpr (MATS == 2)
+            blk = q < 4 ? 4 * ch + q : 8 + 4 * ch + (q - 4);
+        else
+            blk = 8 * ch + q;
+        brow[q] = blk * 16 + (lane & 15);
+    }
+    const int arw = 16 * rg + (lane & 15);
+    const bool active = 16 * rg < rows;  // wave-uniform: this wave's 16 rows hold list entries
+
+    f32x4 acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nch = Kd / kGKC;
+    issue(0);
+    if (nch > 1) issue(1);
+    for (int c = 0; c < nch; ++c) {
+        if (c + 1 < nch)
+            wait_dma<kGDmaPerWave>();  // stage c+1 may still be in flight
+        else
+            wait_dma<0>();
+        __syncthreads();  // every wave's copies of stage c have landed
+        if (c + 2 < nch) issue(c + 2);  // into the stage read at c-1: all waves are past it
+        if (active) {
+            const uint8_t *st = ring + (c % kGStages) * kGStageBytes;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int g = 4 * ks + (lane >> 4);
+                const bf16x8 ah =
+                    __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + arw * 128 + 16 * swz(arw, g)));
+                const bf16x8 al = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + kGABytes + arw * 128 + 16 * swz(arw, g)));
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const bf16x8 bv =
+                        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + brow[q] * 128 + 16 * swz(brow[q], g)));
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, acc[q], 0, 0, 0);
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, acc[q], 0, 0, 0);
+                }
+            }
+        }
+    }
+    if (!active) return;
+
+    // epilogue: acc[q] lane holds weight row (block q, lane % 16) for list rows 16 rg + 4*(lane/16) + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 16 * rg + 4 * (lane >> 4) + i;
+        if (r >= rows) continue;
+        const size_t orow = (size_t)(row0 + r) * N;
+        if constexpr (MATS == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float g = acc[q][i], u = acc[q + 4][i];
+                const float v = (g / (1.0f + expf(-g))) * u;  // silu(g) * u, rabbit2.c:535-537
+                const uint32_t hb = f32_to_bf16_rne(v);
+                const uint32_t lb = f32_to_bf16_rne(v - __uint_as_float(hb << 16));
+                const size_t o = orow + n0 + (4 * ch + q) * 16 + (lane & 15);
+                out_hi[o] = (uint16_t)hb;
+                out_lo[o] = (uint16_t)lb;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) out_f32[orow + n0 + (8 * ch + q) * 16 + (lane & 15)] = acc[q][i];
+        }
+    }
+}
+
+// moe[t][d] = sum_k w[t][k] * y[pos_of[t*K+k]][d] in selection order (rabbit2.c:540); x += moe.
+__global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restrict__ y,
+                                                          const int32_t *__restrict__ pos_of,
+                                                          const float *__restrict__ weights, int K, int D,
+                                                          float *__restrict__ x_inout, float *__restrict__ moe_out) {
+    const int t = blockIdx.y;
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= D) return;
+    float moe = 0.0f;
+    for (int k = 0; k < K; ++k) {
+#pragma clang fp contract(off)
+        const float tmp = y[(size_t)pos_of[t * K + k] * D + d];
+        const float wk = weights[t * K + k];
+        moe = moe + wk * tmp;
+    }
+    const size_t o = (size_t)t * D + d;
+    if (moe_out) moe_out[o] = moe;
+    if (x_inout) x_inout[o] = x_inout[o] + moe;
+}
+
+template <int MATS>
+hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
+                       int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
+                       int topk, const int32_t *counts, const int32_t *offsets, const int32_t *m_off, int E,
+                       int max_mtiles, float *out_f32, uint16_t *out_hi, uint16_t *out_lo) {
+    const long long tiles = (long long)max_mtiles * (N / (kGWRows / MATS));
+    const long long blocks = (tiles + 7) / 8 * 8;
+    if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
+    return launch(L, grouped_gemm_kernel<MATS>, dim3((unsigned)blocks), dim3(512), 0, experts, stride, w_off, w3_off,
+                  N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, out_f32, out_hi, out_lo);
+}
+
+}  // namespace
+
+bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, int H, const void *experts, uint64_t stride,
+                       const float *xb) {
+    return dtype == RBT_DT_BF16 && T >= min_tokens && T <= 65535 && E <= kDispatchMaxE && (long long)T * K <= (1 << 24) &&
+           D % kGWRows == 0 && H % (kGWRows / 2) == 0 && D % kGKC == 0 && H % kGKC == 0 &&
+           (reinterpret_cast<uintptr_t>(experts) & 15u) == 0 && stride % 16 == 0 &&
+           (reinterpret_cast<uintptr_t>(xb) & 15u) == 0;
+}
+
+size_t prefill_workspace_bytes(int T, int E, int K, int D) {
+    const size_t P = (size_t)T * K;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    return up(4 * (size_t)E) + 2 * up(4 * (size_t)(E + 1)) + 2 * up(4 * P) + up(4 * P * (size_t)D) +
+           2 * up(2 * (size_t)T * D);
+}
+
+hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
+                          uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
+                          const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
+                          int32_t **counts_out) {
+    const int P = T * K;
+    uint8_t *w = static_cast<uint8_t *>(ws);
+    auto carve = [&](size_t bytes) {
+        uint8_t *p = w;
+        w += (bytes + 255) / 256 * 256;
+        return p;
+    };
+    int32_t *counts = reinterpret_cast<int32_t *>(carve(4 * (size_t)E));
+    int32_t *offsets = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
+    int32_t *m_off = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
+    int32_t *perm = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
+    int32_t *pos_of = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
+    float *y = reinterpret_cast<float *>(carve(4 * (size_t)P * D));
+    uint16_t *x_hi = reinterpret_cast<uint16_t *>(carve(2 * (size_t)T * D));
+    uint16_t *x_lo = reinterpret_cast<uint16_t *>(carve(2 * (size_t)T * D));
+    // the h planes (bf16 hi, lo; [P][H] each) take the f32 [P][H] h buffer
+    uint16_t *h_hi = reinterpret_cast<uint16_t *>(hbuf), *h_lo = h_hi + (size_t)P * H;
+    if (counts_out) *counts_out = counts;
+    // activation split, then the dispatch: one timed interval (split start .. dispatch end)
+    Launch Ls = Ld, Ldd = Ld;
+    Ls.stop = nullptr;
+    Ldd.start = nullptr;
+    const size_t n8 = (size_t)T * D / 8;
+    const unsigned sblocks = (unsigned)std::min<size_t>((n8 + 255) / 256, 2048);
+    hipError_t e = launch(Ls, split_hilo_kernel, dim3(sblocks), dim3(256), 0, xb, n8, x_hi, x_lo);
+    if (e != hipSuccess) return e;
+    e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off);
+    if (e != hipSuccess) return e;
+    const uint8_t *ex = static_cast<const uint8_t *>(experts);
+    const int max_mtiles = (P + kGRows - 1) / kGRows + E;  // >= sum over experts of ceil(count / 64)
+    // gate/up: N = H, Kd = D, activation rows gathered through perm; h written as hi/lo planes
+    e = launch_gemm<2>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, E,
+                       max_mtiles, nullptr, h_hi, h_lo);
+    if (e != hipSuccess) return e;
+    // down: N = D, Kd = H, activation rows = the h planes in list order
+    e = launch_gemm<1>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets,
+                       m_off, E, max_mtiles, y, nullptr, nullptr);
+    if (e != hipSuccess) return e;
+    return launch(Lc, combine_rows_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)T), dim3(256), 0,
+                  (const float *)y, (const int32_t *)pos_of, weights, K, D, x_inout, moe_out);
+}
+
+}  // namespace rbt

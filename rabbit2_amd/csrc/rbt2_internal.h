@@ -121,6 +121,20 @@ hipError_t launch_experts_decode(const Launch &Lg, const Launch &Ld, int dtype, 
 // fills routing/weights; otherwise it reads routing written by the top-k kernel.
 constexpr int kTopkInGateupMaxE = 64;
 
+// Grouped form for many tokens (bf16 weights): dispatch of the (token, slot) pairs into per-expert
+// lists, gate/up and down as grouped GEMMs on MFMA (every expert's weights read once per call), and
+// the combine in selection order. hbuf [T*K][H]; ws holds prefill_workspace_bytes(). *counts_out
+// receives the device address of the tokens-per-expert histogram. Launch contexts: dispatch,
+// gate/up, down, combine.
+constexpr int kPrefillMinTokensDefault = 16;
+bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, int H, const void *experts,
+                       uint64_t stride, const float *xb);
+size_t prefill_workspace_bytes(int T, int E, int K, int D);
+hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
+                          uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
+                          const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
+                          int32_t **counts_out);
+
 // Dense matvec (one row per wave).
 hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);
 

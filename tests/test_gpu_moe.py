@@ -151,6 +151,10 @@ def test_olmoe_prefill(dev, biased):
         hist = np.bincount(want["routing"].ravel(), minlength=64)
         print("tokens per expert:", hist.tolist(), flush=True)
         assert hist.sum() == 512 * 8
+        # 512 tokens take the grouped path, whose dispatch histogram is exposed through the C ABI
+        counts = dev.expert_counts(64)
+        assert counts is not None
+        assert np.array_equal(counts, np.bincount(got["routing"].ravel(), minlength=64))
         if biased:
             assert hist[:8].sum() > hist[8:].sum()
     finally:

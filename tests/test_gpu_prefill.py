@@ -1,0 +1,142 @@
+"""Parity of the grouped (prefill) MoE path: dispatch, MFMA gate/up and down GEMMs, combine.
+
+Many tokens per call go through per-expert lists instead of per-(token, slot) GEMVs
+(rabbit2_amd/csrc/prefill.hip). The engine evaluates them one token at a time
+(rabbit2/src/rabbit2.c:703-714, MoE block :511-542); per token the result must meet the same bar as
+decode: routing identical except at exact CPU ties, normwise max error <= 1e-3 (tests/common.py).
+The tokens-per-expert histogram must equal the count of the oracle's routing exactly.
+"""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+from tests.common import MOE_RTOL, SynthLayer, normwise_err, routing_check
+
+pytestmark = pytest.mark.gpu
+
+GROUPED_DEFAULT_MIN = 16  # kPrefillMinTokensDefault in rbt2_internal.h
+
+
+@pytest.fixture
+def grouped_from(dev):
+    """Sets the smallest batch that takes the grouped path; restores the default afterwards."""
+    def set_min(n):
+        dev.set_option("prefill_min_tokens", n)
+    yield set_min
+    dev.set_option("prefill_min_tokens", GROUPED_DEFAULT_MIN)
+
+
+def check_grouped(dev, layer, xb, x=None, label=""):
+    dev.set_router_order(po.ORDER_AVX2)
+    want = layer.oracle(xb, po.ORDER_AVX2, x=x)
+    got = layer.run_gpu(xb, x=x)
+    bad, unexplained = routing_check(got["routing"], want["routing"], want["probs"])
+    err = normwise_err(got["moe"], want["moe"])
+    # per-token bar as well: every token's output row meets the tolerance against its own scale
+    tok_err = max(normwise_err(g, w) for g, w in zip(got["moe"], want["moe"])) if len(xb) else 0.0
+    counts = dev.expert_counts(layer.E)
+    hist = np.bincount(got["routing"].ravel(), minlength=layer.E)
+    print(f"{label} T={xb.shape[0]}: routing mismatched tokens {bad} (unexplained {unexplained}), "
+          f"moe err {err:.2e}, worst token err {tok_err:.2e}, max tokens/expert {hist.max()}", flush=True)
+    assert unexplained == 0
+    assert err <= MOE_RTOL
+    assert tok_err <= MOE_RTOL
+    assert counts is not None
+    assert np.array_equal(counts, hist)
+    if bad == 0:
+        assert np.array_equal(counts, np.bincount(want["routing"].ravel(), minlength=layer.E))
+    if x is not None:
+        assert normwise_err(got["x"], want["x"]) <= MOE_RTOL
+    return got, want
+
+
+# (dim, E, K, H, norm_topk, T): whole tiles of 128 (gate/up) / 256 (down) columns
+GROUPED_SHAPES = [
+    (256, 8, 2, 128, 1, 3),      # one column tile each way; most experts see 0-1 pairs
+    (512, 16, 4, 256, 0, 40),    # 160 pairs over 16 experts: partial row tiles
+    (1024, 64, 8, 128, 1, 17),   # E 64, K 8 with 17 tokens: many experts with 1-3 rows
+    (768, 256, 6, 384, 0, 33),   # E 256 (the dispatch maximum), H 384
+    (2048, 64, 8, 1024, 1, 100),  # OLMoE layer, 800 pairs: ~12 rows per expert
+]
+
+
+@pytest.mark.parametrize("shape", GROUPED_SHAPES,
+                         ids=[f"D{s[0]}E{s[1]}K{s[2]}H{s[3]}n{s[4]}T{s[5]}" for s in GROUPED_SHAPES])
+def test_grouped_shapes(dev, grouped_from, shape):
+    D, E, K, H, nt, T = shape
+    grouped_from(1)
+    layer = SynthLayer(dev, D, E, K, H, po.DT_BF16, nt, seed=6, w_scale=1.0, fan_in=True)
+    try:
+        xb = layer.make_x(T, seed=31)
+        x = layer.make_x(T, seed=32, bf16=False)
+        check_grouped(dev, layer, xb, x=x, label=f"grouped D{D}E{E}K{K}H{H}")
+    finally:
+        layer.close()
+
+
+def test_grouped_matches_gemv_path(dev, grouped_from):
+    """The same 24 tokens through the grouped path and the per-pair GEMV path: same routing and
+    weights (the router is shared), outputs within the bar of each other and of the oracle."""
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=1)
+    try:
+        xb = layer.make_x(24, seed=8)
+        grouped_from(1)
+        g, want = check_grouped(dev, layer, xb, label="grouped")
+        grouped_from(1 << 16)
+        v = layer.run_gpu(xb)
+        assert np.array_equal(g["routing"], v["routing"])
+        assert np.array_equal(g["weights"], v["weights"])
+        assert normwise_err(v["moe"], want["moe"]) <= MOE_RTOL
+        assert normwise_err(g["moe"], v["moe"]) <= MOE_RTOL
+    finally:
+        layer.close()
+
+
+def test_grouped_one_hot_expert_set(dev, grouped_from):
+    """Every token routed to the same 8 experts (+30 on their router logits): 8 lists of 300 rows,
+    5 row tiles each, 56 experts empty."""
+    grouped_from(1)
+    bias = np.zeros(64, np.float32)
+    bias[10:18] = 30.0
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 0, seed=2, bias=bias)
+    try:
+        xb = layer.make_x(300, seed=9)
+        got, _ = check_grouped(dev, layer, xb, label="hot set")
+        counts = dev.expert_counts(64)
+        assert counts[10:18].tolist() == [300] * 8 and counts.sum() == 2400
+    finally:
+        layer.close()
+
+
+def test_grouped_deterministic(dev, grouped_from):
+    grouped_from(1)
+    layer = SynthLayer(dev, 1024, 64, 8, 128, po.DT_BF16, 1, seed=3)
+    try:
+        xb = layer.make_x(64, seed=10)
+        a = layer.run_gpu(xb)
+        b = layer.run_gpu(xb)
+        assert a["moe"].tobytes() == b["moe"].tobytes()
+        assert np.array_equal(a["routing"], b["routing"])
+    finally:
+        layer.close()
+
+
+def test_grouped_not_taken_for_f32(dev, grouped_from):
+    """f32 weights stay on the GEMV path (the MFMA path multiplies bf16 weights); results still meet
+    the bar."""
+    grouped_from(1)
+    layer = SynthLayer(dev, 256, 8, 2, 256, po.DT_F32, 1, seed=4, w_scale=1.0, fan_in=True)
+    try:
+        xb = layer.make_x(20, seed=12)
+        want = layer.oracle(xb, po.ORDER_AVX2)
+        dev.set_router_order(po.ORDER_AVX2)
+        got = layer.run_gpu(xb)
+        assert routing_check(got["routing"], want["routing"], want["probs"])[1] == 0
+        assert normwise_err(got["moe"], want["moe"]) <= MOE_RTOL
+    finally:
+        layer.close()
+
+
+def test_prefill_min_tokens_option_checked(dev):
+    with pytest.raises(Exception):
+        dev.set_option("prefill_min_tokens", 0)
