@@ -61,10 +61,15 @@ void rbt_hip_free(rbt_hip *h);
 /* Last error message of this handle ("" if none); with h == NULL, the last init failure. */
 const char *rbt_hip_last_error(const rbt_hip *h);
 int rbt_hip_set_router_order(rbt_hip *h, int order);
-/* Tuning switch (no counterpart in the reference):
- *   "fused_decode"  1 (default): a batch-1 block of up to 64 experts runs the softmax + top-k inside
- *                   the expert gate/up kernel (router logits, gate/up, down: three launches);
- *                   0: a separate top-k launch (four launches). Results are identical. */
+/* Tuning switches (no counterpart in the reference):
+ *   "fused_decode"        1 (default): a batch-1 block of up to 64 experts runs the softmax + top-k
+ *                         inside the expert gate/up kernel (router logits, gate/up, down: three
+ *                         launches); 0: a separate top-k launch (four launches). Same results.
+ *   "prefill_min_tokens"  smallest T (1..65536, default 16) that takes the grouped path for bf16
+ *                         weights: (token, slot) pairs dispatched into per-expert lists and the
+ *                         expert FFN run as grouped GEMMs on the matrix cores, each expert's weights
+ *                         read once per call. Smaller T runs one GEMV per pair. Routing is the same
+ *                         either way; outputs agree within the parity tolerance. */
 int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
 
 /* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the
@@ -115,7 +120,9 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
 /* ---- instrumentation (the reference's only timing is its stderr tok/s line, rabbit2.c:742-744) ----
  * While enabled, every kernel launch of rbt_hip_moe_dev is bracketed by HIP events on the handle
  * stream and its duration is accumulated under its name ("router", "topk", "gateup",
- * "down_combine"); each call then waits for its own work. rbt_hip_profile_get returns 0 for an unknown
+ * "down_combine"; the grouped path adds "dispatch" -- the activation hi/lo split and the per-expert
+ * lists -- and "combine", and its "down_combine" is the down GEMM alone); each call then waits for
+ * its own work. rbt_hip_profile_get returns 0 for an unknown
  * name. Meant for measurement passes, not for the timed hot loop. */
 int rbt_hip_profile_enable(rbt_hip *h, int on);
 int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches);

@@ -185,6 +185,115 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 
 }
 
+// Many tokens, AVX2 order: the router tile is shared by a block's tokens instead of re-read per token.
+// grid (ceil(E/16), ceil(T/8)), 256 threads: tid -> half h = tid & 1, router row 16*bx + ((tid >> 1) & 15),
+// token 8*by + (tid >> 5). Thread (t, r, h) runs chains 8h..8h+7 of row r for token t: step m adds the
+// rounded products of columns 16m + 8h + j (j = 0..7), i.e. chain 8h+j, in column order -- a 16-byte
+// read of the row and two of x per step, 8 independent chains. The pair (h = 0, 1) sits in adjacent
+// lanes; the h = 0 lane combines (chain j) + (chain 8+j) for j = 0..7 onto 0.0f, then the tail.
+// LDS per column chunk of kBCols: router rows [16][kBCols] in DT and x [8][kBCols] f32.
+constexpr int kBRows = 16, kBTok = 8, kBCols = 512;
+template <int DT>
+__global__ __launch_bounds__(256) void router_logits_batch_kernel(const float *__restrict__ xb,
+                                                                  const void *__restrict__ Wv,
+                                                                  const float *__restrict__ bias, int T, int E, int D,
+                                                                  float *__restrict__ logits) {
+    using W = typename RouterTile<DT, false>::W;
+    constexpr int ESZ = (int)sizeof(W);
+    constexpr int WP = kBCols * ESZ + 32;  // row pitch in bytes (32-byte pad)
+    constexpr int XP = kBCols * 4 + 16;
+    __shared__ __align__(16) unsigned char wt[kBRows * WP];
+    __shared__ __align__(16) unsigned char xt[kBTok * XP];
+    const W *Wg = static_cast<const W *>(Wv);
+    const int tid = threadIdx.x, h = tid & 1, rl = (tid >> 1) & 15, tl = tid >> 5;
+    const int r0 = blockIdx.x * kBRows, t0 = blockIdx.y * kBTok;
+    const int r = r0 + rl, t = t0 + tl;
+    const int nrows = min(kBRows, E - r0), ntok = min(kBTok, T - t0);
+    const int body = (D / 16) * 16;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    for (int c0 = 0; c0 < body; c0 += kBCols) {
+        const int cn = min(kBCols, body - c0);  // a multiple of 16
+        // stage: 16-byte units, every load of a batch issued before the stores (clamped addresses)
+        {
+            constexpr int per = 16 / ESZ;
+            const int wu = cn / per, wtot = nrows * wu;
+            const int xu = cn / 4, xtot = ntok * xu;
+            for (int b0 = tid; b0 < wtot + xtot; b0 += 256 * 8) {
+                u32x4 v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int u = min(b0 + i * 256, wtot + xtot - 1);
+                    if (u < wtot) {
+                        const int rr = u / wu, k = u - rr * wu;
+                        v[i] = *reinterpret_cast<const u32x4 *>(Wg + (size_t)(r0 + rr) * D + c0 + k * per);
+                    } else {
+                        const int q = u - wtot, tt = q / xu, k = q - tt * xu;
+                        v[i] = *reinterpret_cast<const u32x4 *>(xb + (size_t)(t0 + tt) * D + c0 + 4 * k);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int u = b0 + i * 256;
+                    if (u < wtot) {
+                        const int rr = u / wu, k = u - rr * wu;
+                        *reinterpret_cast<u32x4 *>(wt + rr * WP + k * 16) = v[i];
+                    } else if (u < wtot + xtot) {
+                        const int q = u - wtot, tt = q / xu, k = q - tt * xu;
+                        *reinterpret_cast<u32x4 *>(xt + tt * XP + k * 16) = v[i];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (rl < nrows && tl < ntok) {
+            const unsigned char *wr = wt + rl * WP + h * 8 * ESZ;
+            const float *xr = reinterpret_cast<const float *>(xt + tl * XP) + 8 * h;
+            const int steps = cn / 16;
+#pragma unroll 2
+            for (int m = 0; m < steps; ++m) {
+                float wv[8];
+                if constexpr (DT == RBT_DT_F32) {
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(wr + m * 64);
+                    const f32x4 b = *reinterpret_cast<const f32x4 *>(wr + m * 64 + 16);
+                    wv[0] = a.x; wv[1] = a.y; wv[2] = a.z; wv[3] = a.w;
+                    wv[4] = b.x; wv[5] = b.y; wv[6] = b.z; wv[7] = b.w;
+                } else {
+                    const u32x4 a = *reinterpret_cast<const u32x4 *>(wr + m * 32);
+                    wv[0] = bf16_lo(a.x); wv[1] = bf16_hi(a.x); wv[2] = bf16_lo(a.y); wv[3] = bf16_hi(a.y);
+                    wv[4] = bf16_lo(a.z); wv[5] = bf16_hi(a.z); wv[6] = bf16_lo(a.w); wv[7] = bf16_hi(a.w);
+                }
+                const f32x4 xa = *reinterpret_cast<const f32x4 *>(xr + 16 * m);
+                const f32x4 xc = *reinterpret_cast<const f32x4 *>(xr + 16 * m + 4);
+                acc[0] = acc[0] + wv[0] * xa.x;
+                acc[1] = acc[1] + wv[1] * xa.y;
+                acc[2] = acc[2] + wv[2] * xa.z;
+                acc[3] = acc[3] + wv[3] * xa.w;
+                acc[4] = acc[4] + wv[4] * xc.x;
+                acc[5] = acc[5] + wv[5] * xc.y;
+                acc[6] = acc[6] + wv[6] * xc.z;
+                acc[7] = acc[7] + wv[7] * xc.w;
+            }
+        }
+        __syncthreads();
+    }
+    // chains 8..15 from the partner lane (h = 1), fetched by every lane (the DPP move is wave-wide)
+    float other[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) other[j] = dpp_f<kDppXor1>(acc[j]);
+    if (h == 0 && rl < nrows && tl < ntok) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum = sum + (acc[j] + other[j]);
+        const W *wrow = Wg + (size_t)r * D;
+        const float *x = xb + (size_t)t * D;
+        for (int i = body; i < D; ++i) sum = sum + widen<DT>(wrow[i]) * x[i];
+        if (bias) sum = sum + bias[r];
+        logits[(size_t)t * E + r] = sum;
+    }
+}
+
 // grid (T), block 64 or 256 threads; dynamic LDS E floats when E <= kLdsProbsMax. Reads the logits
 // row of its token, leaves the probabilities in it, writes routing/weights.
 __global__ __launch_bounds__(256) void router_topk_kernel(int E, int K, int norm_topk, float *__restrict__ probs,
@@ -308,15 +417,28 @@ hipError_t launch_logits(const Launch &L, const float *xb, const void *W, const 
                   (uint32_t)lds, xb, W, bias, E, D, rpb, vec ? 1 : 0, probs);
 }
 
+// The batch kernel (AVX2 order) from 16 tokens on; its 16-byte staging needs 16-byte aligned rows.
+inline bool batch_ok(int T, int D, int dtype, const void *W, const float *xb) {
+    const int esz = dtype == RBT_DT_BF16 ? 2 : 4;
+    return T >= 16 && (reinterpret_cast<uintptr_t>(W) % 16 == 0) && (reinterpret_cast<uintptr_t>(xb) % 16 == 0) &&
+           (D * esz) % 16 == 0 && D % 4 == 0;
+}
+
 template <int NCH, int DT>
 hipError_t launch_t(const Launch &L, const Launch &Lk, const float *xb, const void *W, const float *bias, int T, int E,
                     int D, int K, int norm_topk, float *probs, int32_t *routing, float *weights) {
-    // 64-thread blocks for small batches (4 or 16 rows each, so one token's router spreads over many
-    // CUs); 256 threads (16 rows) for larger batches with the AVX2 order.
-    const int threads = (NCH == 16 && T > 8) ? 256 : 64;
-    const bool wide = threads / NCH <= 4;
-    hipError_t e = wide ? launch_logits<NCH, DT, true>(L, xb, W, bias, T, E, D, threads, probs)
-                        : launch_logits<NCH, DT, false>(L, xb, W, bias, T, E, D, threads, probs);
+    hipError_t e;
+    if (NCH == 16 && batch_ok(T, D, DT, W, xb)) {
+        e = launch(L, router_logits_batch_kernel<DT>, dim3((E + kBRows - 1) / kBRows, (T + kBTok - 1) / kBTok),
+                   dim3(256), 0, xb, W, bias, T, E, D, probs);
+    } else {
+        // 64-thread blocks for small batches (4 or 16 rows each, so one token's router spreads over
+        // many CUs); 256 threads (16 rows) for larger batches with the AVX2 order.
+        const int threads = (NCH == 16 && T > 8) ? 256 : 64;
+        const bool wide = threads / NCH <= 4;
+        e = wide ? launch_logits<NCH, DT, true>(L, xb, W, bias, T, E, D, threads, probs)
+                 : launch_logits<NCH, DT, false>(L, xb, W, bias, T, E, D, threads, probs);
+    }
     if (e != hipSuccess) return e;
     const int tk = E <= 64 ? 64 : 256;
     const size_t lds_k = E <= kLdsProbsMax ? (size_t)E * 4 : 0;
@@ -331,6 +453,14 @@ hipError_t launch_router_logits(const Launch &L, int order, int dtype, const flo
     if (T <= 0) return hipSuccess;
     if (T > 65535) return hipErrorInvalidValue;
     if (order == RBT_ORDER_AVX2) {
+        if (batch_ok(T, D, dtype, W, xb))
+            return dtype == RBT_DT_BF16
+                       ? launch(L, router_logits_batch_kernel<RBT_DT_BF16>,
+                                dim3((E + kBRows - 1) / kBRows, (T + kBTok - 1) / kBTok), dim3(256), 0, xb, W, bias, T,
+                                E, D, logits)
+                       : launch(L, router_logits_batch_kernel<RBT_DT_F32>,
+                                dim3((E + kBRows - 1) / kBRows, (T + kBTok - 1) / kBTok), dim3(256), 0, xb, W, bias, T,
+                                E, D, logits);
         const int threads = T > 8 ? 256 : 64;
         if (dtype == RBT_DT_BF16)
             return threads == 64 ? launch_logits<16, RBT_DT_BF16, true>(L, xb, W, bias, T, E, D, 64, logits)

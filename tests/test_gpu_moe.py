@@ -159,3 +159,28 @@ def test_olmoe_prefill(dev, biased):
             assert hist[:8].sum() > hist[8:].sum()
     finally:
         layer.close()
+
+
+# Batches of 16+ tokens take the batched router kernel (AVX2 order): the router tile is staged once per
+# 8 tokens in 512-column chunks. Shapes: f32 with a 4-column tail, bf16 with an 8-column tail after a
+# full and a partial chunk, f32 with a last chunk of 16 columns, and E not a multiple of 16.
+ROUTER_BATCH_SHAPES = [
+    (100, 8, 2, 16, po.DT_F32, 1),
+    (536, 8, 3, 16, po.DT_BF16, 0),
+    (1040, 6, 2, 16, po.DT_F32, 1),
+    (2048, 20, 4, 16, po.DT_BF16, 1),
+]
+
+
+@pytest.mark.parametrize("shape", ROUTER_BATCH_SHAPES,
+                         ids=[f"D{s[0]}E{s[1]}K{s[2]}dt{s[4]}" for s in ROUTER_BATCH_SHAPES])
+def test_router_batch_shapes(dev, shape):
+    D, E, K, H, dt, nt = shape
+    bias = np.linspace(-0.5, 0.5, E).astype(np.float32)
+    layer = SynthLayer(dev, D, E, K, H, dt, nt, seed=9, w_scale=1.0, fan_in=True, bias=bias)
+    try:
+        for T in (16, 29):
+            xb = layer.make_x(T, seed=50 + T, bf16=False)
+            check(layer, xb, po.ORDER_AVX2, dev, label=f"router batch D{D}E{E}")
+    finally:
+        layer.close()
