@@ -12,8 +12,10 @@ selected experts change from step to step. Only the MoE blocks are timed (the at
 the model is not part of this path).
 
 Prints one JSON line: tok/s of the 16-layer MoE stack; the roofline of the dominant kernel
-(expert gate/up GEMV) from HIP events on the stream it runs on; the whole-layer HBM rate; and the
-CPU baseline (the oracle's AVX2-order path on one host core, the engine's own arithmetic).
+(expert gate/up GEMV) from HIP events on the stream it runs on; the whole-layer HBM rate; the
+512-token prefill of layer 0 ("prefill": uniform and skewed routing, tokens-per-expert histogram,
+HBM rate and matrix-core utilisation of the grouped GEMMs); and the CPU baseline (the oracle's
+AVX2-order path on one host core, the engine's own arithmetic).
 """
 import argparse
 import ctypes as C
@@ -88,6 +90,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch every layer from Python instead of replaying a "
                     "captured HIP graph of the steps")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target length of the CPU baseline sample")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill leg")
+    ap.add_argument("--prefill-reps", type=int, default=20, help="timed calls per prefill workload")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one device-to-device copy of this size (a known-size kernel for scaling "
                          "FETCH_SIZE/WRITE_SIZE counters)")
@@ -140,6 +144,17 @@ def main():
 
     hipapi, mk, elapsed = hip_events()
     stream = C.c_void_p(dev.stream)
+    if args.copy_calib_mib:
+        # one device-to-device copy of known size (the runtime's blit kernel reads and writes exactly
+        # this many bytes), for scaling the FETCH_SIZE / WRITE_SIZE counters of a --pmc run
+        nb = args.copy_calib_mib << 20
+        src, dst = dev.malloc(nb), dev.malloc(nb)
+        dev.memset(src, 1)
+        hipapi.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        assert hipapi.hipMemcpyAsync(dst.p, src.p, nb, 3, stream) == 0  # hipMemcpyDeviceToDevice
+        dev.synchronize()
+        dev.free(src)
+        dev.free(dst)
     # A decode engine replays a captured graph per token; one graph here holds GRAPH_STEPS steps so
     # the 64 input vectors are all cycled through (kernels only: no memset/copy nodes).
     GRAPH_STEPS = NX // LAYERS
@@ -217,7 +232,7 @@ def main():
     # HBM bytes per launch of the dominant kernel, from the calibrated rocprofv3 --pmc runs kept
     # under profiles/ (counters cannot be read from inside this process)
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "olmoe_moe_decode_bs1_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "olmoe_moe_layer_traffic.json")
     if os.path.exists(tpath):
         try:
             traffic = json.load(open(tpath))["per_launch"][TRAFFIC_KEY[dom_name]]["bytes"]
@@ -254,7 +269,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "traffic_source": "profiles/olmoe_moe_decode_bs1_traffic.json" if traffic else None,
+            "traffic_source": "profiles/olmoe_moe_layer_traffic.json" if traffic else None,
             "alg_bytes_per_launch": alg_bytes[dom_name],
             "avg_launch_us": round(dom["avg_us"], 3),
         },
@@ -271,11 +286,116 @@ def main():
         "setup_s": round(fill_s, 2),
     }
 
+    if not args.no_prefill:
+        out["prefill"] = prefill_leg(dev, routers, experts, stride, args.prefill_reps, not args.no_cpu)
+
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(dev, routers, experts, stride, xs_host, args.cpu_seconds)
 
     print(json.dumps(out), flush=True)
     dev.close()
+
+
+PREFILL_T = 512
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, published
+PREFILL_KERNELS = ("router", "topk", "dispatch", "gateup", "down_combine", "combine")
+
+
+def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
+    """512 tokens through one OLMoE-shaped MoE layer (layer 0 of the decode stack): once with the
+    plain router and once with +2.0 on the router logits of experts 0-7 (skewed load). Reports the
+    per-call time, per-kernel times (HIP events), the tokens-per-expert histogram of the dispatch,
+    the layer's algorithmic HBM rate and the grouped GEMMs' matrix-core utilisation."""
+    from rabbit2_amd import hip as rh
+    T = PREFILL_T
+    P = T * K
+    xraw = dev.malloc(T * D * 2)
+    dev.fill_normal(xraw, rh.DT_BF16, T * D, SEED, 0x5EED + 1)
+    xs = (dev.d2h(xraw, (T * D,), np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(T, D)
+    dev.free(xraw)
+    xb = dev.upload_array(xs)
+    moe = dev.malloc(T * D * 4)
+    bias_dev = dev.upload_array(np.array([2.0] * 8 + [0.0] * (E - 8), np.float32))
+    # algorithmic totals of the layer (every expert touched once, router, x in, moe out)
+    esz = 2
+    alg_bytes = E * 3 * H * D * esz + E * D * esz + T * D * 2 + T * D * 4
+    alg_flops = T * 2 * E * D + P * 6 * H * D
+    gemm_flops = {"gateup": P * 4 * H * D, "down_combine": P * 2 * H * D}
+    res = {}
+    for name, bias in (("uniform", None), ("skewed", bias_dev)):
+        L = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride, bias)  # layer 0
+        dev.reserve(L, T)
+        for _ in range(3):
+            dev.moe_dev(L, xb, T, moe=moe)
+        dev.synchronize()
+        hipapi, mk, elapsed = hip_events()
+        stream = C.c_void_p(dev.stream)
+        e0, e1 = mk(), mk()
+        hipapi.hipEventRecord(e0, stream)
+        for _ in range(reps):
+            dev.moe_dev(L, xb, T, moe=moe)
+        hipapi.hipEventRecord(e1, stream)
+        us = 1000.0 * elapsed(e0, e1) / reps
+        dev.profile(True)
+        for _ in range(reps):
+            dev.moe_dev(L, xb, T, moe=moe)
+        kern = {}
+        for kname in PREFILL_KERNELS:
+            tot, n = dev.profile_get(kname)
+            if n:
+                kern[kname] = {"avg_us": round(1000.0 * tot / n, 2)}
+        dev.profile(False)
+        counts = dev.expert_counts(E)
+        tiles = int(sum((c + 63) // 64 for c in counts))
+        for kname, fl in gemm_flops.items():
+            if kname in kern:
+                t = kern[kname]["avg_us"] * 1e-6
+                # issued: every 64-row tile runs in full, and each product is two bf16 MFMAs (hi + lo part)
+                issued = 2 * fl * (tiles * 64) / P
+                kern[kname]["mfma_util_alg"] = round(fl / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+                kern[kname]["mfma_util_issued"] = round(issued / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+                wbytes = E * (2 if kname == "gateup" else 1) * H * D * esz
+                kern[kname]["weight_GBps"] = round(wbytes / t / 1e9, 1)
+        res[name] = {
+            "us_per_call": round(us, 2),
+            "tok_per_s": round(T / (us * 1e-6), 1),
+            "hbm_GBps_alg": round(alg_bytes / (us * 1e-6) / 1e9, 1),
+            "hbm_frac_alg": round(alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "mfma_util_alg": round(alg_flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "kernels": kern,
+            "tokens_per_expert": [int(c) for c in counts],
+            "row_tiles": tiles,
+        }
+    out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,
+           "note": "per-call time of the whole MoE block (router .. combine), eager launches, inputs in HBM",
+           **res}
+    if with_cpu:
+        out["cpu_baseline"] = cpu_prefill(dev, routers, experts, stride, xs, 64)
+    for b in (xb, moe, bias_dev):
+        dev.free(b)
+    return out
+
+
+def cpu_prefill(dev, routers, experts, stride, xs, n):
+    """The engine evaluates a prompt token by token (rabbit2.c:703-714): the oracle's AVX2-order MoE
+    layer on one host core over n of the prefill tokens, as tok/s."""
+    from oracle import pyoracle as po
+    router = dev.d2h(routers, (E, D), np.uint16)  # layer 0
+    ex = dev.d2h(experts, (E * stride,), np.uint8)
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {sorted(old)[0]})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        t0 = time.perf_counter()
+        po.moe_layer(D, E, K, H, po.DT_BF16, 1, router, ex, stride, xs[:n], order=po.ORDER_AVX2)
+        dt = time.perf_counter() - t0
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    return {"value": round(n / dt, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{n} of the 512 prefill tokens through the layer ({dt:.2f} s)"}
 
 
 def cpu_baseline(dev, routers, experts, stride, xs, seconds):
@@ -294,7 +414,7 @@ def cpu_baseline(dev, routers, experts, stride, xs, seconds):
         t0 = time.perf_counter()
         po.moe_layer(D, E, K, H, po.DT_BF16, 1, router, ex, stride, xs[:1], order=po.ORDER_AVX2)
         t1 = time.perf_counter() - t0
-        n = int(max(3, min(len(xs) * 4, seconds / max(t1, 1e-6))))
+        n = int(max(3, min(20000, seconds / max(t1, 1e-6))))  # about `seconds` of CPU work
         xin = np.stack([xs[i % len(xs)] for i in range(n)])
         t0 = time.perf_counter()
         po.moe_layer(D, E, K, H, po.DT_BF16, 1, router, ex, stride, xin, order=po.ORDER_AVX2)

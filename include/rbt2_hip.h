@@ -65,7 +65,7 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *   "fused_decode"        1 (default): a batch-1 block of up to 64 experts runs the softmax + top-k
  *                         inside the expert gate/up kernel (router logits, gate/up, down: three
  *                         launches); 0: a separate top-k launch (four launches). Same results.
- *   "prefill_min_tokens"  smallest T (1..65536, default 16) that takes the grouped path for bf16
+ *   "prefill_min_tokens"  smallest T (1..65536, default 12) that takes the grouped path for bf16
  *                         weights: (token, slot) pairs dispatched into per-expert lists and the
  *                         expert FFN run as grouped GEMMs on the matrix cores, each expert's weights
  *                         read once per call. Smaller T runs one GEMV per pair. Routing is the same

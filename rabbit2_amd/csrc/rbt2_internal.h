@@ -126,7 +126,7 @@ constexpr int kTopkInGateupMaxE = 64;
 // the combine in selection order. hbuf [T*K][H]; ws holds prefill_workspace_bytes(). *counts_out
 // receives the device address of the tokens-per-expert histogram. Launch contexts: dispatch,
 // gate/up, down, combine.
-constexpr int kPrefillMinTokensDefault = 16;
+constexpr int kPrefillMinTokensDefault = 12;  // measured crossover with the per-pair GEMVs (OLMoE layer)
 bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, int H, const void *experts,
                        uint64_t stride, const float *xb);
 size_t prefill_workspace_bytes(int T, int E, int K, int D);

@@ -14,7 +14,7 @@ from tests.common import MOE_RTOL, SynthLayer, normwise_err, routing_check
 
 pytestmark = pytest.mark.gpu
 
-GROUPED_DEFAULT_MIN = 16  # kPrefillMinTokensDefault in rbt2_internal.h
+GROUPED_DEFAULT_MIN = 12  # kPrefillMinTokensDefault in rbt2_internal.h
 
 
 @pytest.fixture
