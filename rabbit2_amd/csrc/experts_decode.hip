@@ -21,6 +21,7 @@ namespace rbt {
 namespace {
 
 constexpr int KMAX_T = 64;  // selected experts per token (the engine's MAX_TOPK, rabbit2.c:59)
+constexpr int kHStageMax = 16;  // 16-byte units of h per thread in the down kernel: K*H <= 16384 floats
 constexpr int EMAX_T = 64;  // experts per layer for the in-kernel top-k (one per lane of wave 0)
 
 // Softmax + top-k of one token's logits, the engine's arithmetic (rabbit2.c:399-405, :516-528,
@@ -29,12 +30,26 @@ constexpr int EMAX_T = 64;  // experts per layer for the in-kernel top-k (one pe
 // LDS with wave-scope fences only (a wave's LDS operations execute in order).
 __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
-__device__ void block_topk(const float *__restrict__ logits, int E, int K, int norm_topk, float *s_v, int *s_idx,
-                           float *s_pw, float *s_w, float *s_sum) {
-    (void)s_sum;
+// XS > 0: the block also stages the token's activation row x (xu 16-byte units, at most XS per
+// thread, clamped loads and stores) into xs_lds; its loads are issued next to the logits load, so
+// they land while wave 0 ranks.
+template <int XS = 0>
+__device__ __forceinline__ void block_topk(const float *__restrict__ logits, int E, int K, int norm_topk, float *s_v, int *s_idx,
+                           float *s_pw, float *s_w, const float *__restrict__ x = nullptr, f32x4 *xs_lds = nullptr,
+                           int xu = 0) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    f32x4 xv[XS > 0 ? XS : 1];
+    if constexpr (XS > 0) {
+#pragma unroll
+        for (int i = 0; i < XS; ++i) xv[i] = reinterpret_cast<const f32x4 *>(x)[min(tid + i * (int)blockDim.x, xu - 1)];
+    }
+    const float v0 = (tid < kWave && lane < E) ? logits[lane] : -INFINITY;
+    if constexpr (XS > 0) {
+#pragma unroll
+        for (int i = 0; i < XS; ++i) xs_lds[min(tid + i * (int)blockDim.x, xu - 1)] = xv[i];
+    }
     if (tid < kWave) {
-        const float v = lane < E ? logits[lane] : -INFINITY;
+        const float v = v0;
         float mx = wave_max(v);  // ignores NaN like the engine's '>' scan ...
         const float first = lane_value(v, 0);
         if (first != first) mx = first;  // ... which starts from element 0
@@ -124,6 +139,8 @@ __device__ __forceinline__ float dot16r(const u32x4 w, const f32x4 x0, const f32
 // TOPK (batch 1 only): every block first runs the token's softmax + top-k from the router logits
 // (`logits`, E experts) instead of reading `routing`; block 0 publishes routing/weights for the
 // down kernel. Saves a launch on the decode critical path.
+// With TOPK (one token) the block stages x in LDS once (XS units per thread) instead of every wave
+// reading all of it from L2.
 template <int DT, int NC, int JW, bool TOPK>
 __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
                                                           int32_t *__restrict__ routing,
@@ -133,14 +150,16 @@ __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restr
                                                           float *__restrict__ weights) {
     constexpr int kEsz = Elem<DT>::kEsz, kPer = Elem<DT>::kPer;
     constexpr int D = NC * kWave * kPer;
+    constexpr int XS = TOPK ? (D / 4 + 255) / 256 : 0;  // x units per thread (D <= 4096: at most 4)
+    __shared__ __align__(16) f32x4 xs_lds[TOPK ? D / 4 : 1];
     const int lane = threadIdx.x & (kWave - 1);
     const long long item = (long long)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
     int e;
     if constexpr (TOPK) {
         __shared__ __align__(16) float s_v[EMAX_T];
         __shared__ int s_idx[KMAX_T];
-        __shared__ float s_pw[KMAX_T], s_w[KMAX_T], s_sum;
-        block_topk(logits, E, K, norm_topk, s_v, s_idx, s_pw, s_w, &s_sum);
+        __shared__ float s_pw[KMAX_T], s_w[KMAX_T];
+        block_topk<XS>(logits, E, K, norm_topk, s_v, s_idx, s_pw, s_w, xb, xs_lds, D / 4);
         if (blockIdx.x == 0 && (int)threadIdx.x < K) {
             routing[threadIdx.x] = s_idx[threadIdx.x];
             weights[threadIdx.x] = s_w[threadIdx.x];
@@ -171,7 +190,7 @@ __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restr
         }
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
-        const float *xp = x + (lane + kWave * i) * kPer;
+        const float *xp = (XS > 0 ? reinterpret_cast<const float *>(xs_lds) : x) + (lane + kWave * i) * kPer;
         x0[i] = *reinterpret_cast<const f32x4 *>(xp);
         if constexpr (DT == RBT_DT_BF16) x1[i] = *reinterpret_cast<const f32x4 *>(xp + 4);
     }
@@ -196,7 +215,8 @@ __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restr
 }
 
 // grid (ceil(D / (4*RW)), T), block 256, dynamic LDS K*H*4 bytes; requires H == NH * 64 * kPer.
-template <int DT, int NH, int RW>
+// HS: 16-byte units of h staged per thread (K*H/4 <= 256*HS).
+template <int DT, int NH, int RW, int HS>
 __global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
                                                         const int32_t *__restrict__ routing,
                                                         const float *__restrict__ weights,
@@ -216,8 +236,18 @@ __global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restric
     const int nr = D - dbase < RW ? D - dbase : RW;
     const int32_t *rt = routing + (size_t)t * K;
 
-    // The weight loads of the first slot chunk go out first: they only need the expert ids, so
-    // they are in flight while h is staged.
+    // Load order: this thread's share of h first (small, from L2), then the weight loads of the first
+    // slot chunk, then the h stores to LDS. Loads complete in issue order, so the stores wait only for
+    // the h loads while every weight load is in flight, and the dot products below can start as
+    // soon as the first weights land instead of after the whole stream.
+    const f32x4 *hsrc = reinterpret_cast<const f32x4 *>(hbuf + (size_t)t * K * H);
+    f32x4 *hdst = reinterpret_cast<f32x4 *>(hs);
+    const int units = K * H / 4;  // 16-byte units of h, at most HS per thread
+    f32x4 hv[HS];
+#pragma unroll
+    for (int i = 0; i < HS; ++i) hv[i] = hsrc[min(tid + i * (int)blockDim.x, units - 1)];
+    const float wsel = weights[(size_t)t * K + min(tid & 63, K - 1)];
+
     u32x4 w[KC][RW][NH];
     auto load_chunk = [&](int k0, int nk) {
 #pragma unroll
@@ -234,36 +264,22 @@ __global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restric
         }
     };
     load_chunk(0, K < KC ? K : KC);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // stage h of this token: K*H/4 16-byte units, 8 in flight per thread
-    {
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(hbuf + (size_t)t * K * H);
-        f32x4 *dst = reinterpret_cast<f32x4 *>(hs);
-        const int units = K * H / 4;
-        for (int b0 = tid; b0 < units; b0 += blockDim.x * 8) {
-            f32x4 v[8];
+    __builtin_amdgcn_sched_barrier(0);  // all weight loads issued before the h stores wait on h
+    // unconditional stores (clamped lanes rewrite the last unit with the same data): a store behind a
+    // branch would let the compiler sink its load into the branch, after the weight stream
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = src[min(b0 + i * (int)blockDim.x, units - 1)];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (b0 + i * (int)blockDim.x < units) dst[b0 + i * blockDim.x] = v[i];
-        }
-    }
-    if (tid < K) s_w[tid] = weights[(size_t)t * K + tid];
+    for (int i = 0; i < HS; ++i) hdst[min(tid + i * (int)blockDim.x, units - 1)] = hv[i];
+    s_w[tid & 63] = wsel;  // entries past K hold weight K-1 and are never read
     __syncthreads();
-    if (!active) return;  // no barrier follows
 
+    // The first chunk is consumed in straight-line code right after the barrier, and waves past D work
+    // on clamped rows and only skip the final store: the weights are read-only to this kernel, so the
+    // compiler may move their loads anywhere before the first use, and a use behind a branch (an
+    // early exit, a loop) would let it sink them below the barrier, serialising the stream.
     float moe[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) moe[r] = 0.0f;
-
-    for (int k0 = 0; k0 < K; k0 += KC) {
-        const int nk = K - k0 < KC ? K - k0 : KC;
-        if (k0 > 0) {
-            load_chunk(k0, nk);
-            __builtin_amdgcn_sched_barrier(0);  // every weight load of the chunk is issued before any use
-        }
+    auto process = [&](int k0, int nk) {
         float acc[KC][RW];
 #pragma unroll
         for (int kk = 0; kk < KC; ++kk) {
@@ -290,8 +306,15 @@ __global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restric
                 moe[r] = moe[r] + wk * acc[kk][r];  // rabbit2.c:540, rounded product then add
             }
         }
+    };
+    process(0, K < KC ? K : KC);
+    for (int k0 = KC; k0 < K; k0 += KC) {
+        const int nk = K - k0 < KC ? K - k0 : KC;
+        load_chunk(k0, nk);
+        __builtin_amdgcn_sched_barrier(0);  // every weight load of the chunk is issued before any use
+        process(k0, nk);
     }
-    if (lane == 0) {
+    if (lane == 0 && active) {
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
             if (r < nr) {
@@ -323,9 +346,17 @@ hipError_t down_nh(const Launch &L, const uint8_t *E, uint64_t stride, const int
                    const float *hbuf, int T, int K, int D, float *x_inout, float *moe_out) {
     constexpr int RW = 2;
     constexpr int H = NH * kWave * Elem<DT>::kPer;
-    return launch(L, down_fast_kernel<DT, NH, RW>, dim3((unsigned)((D + 4 * RW - 1) / (4 * RW)), (unsigned)T),
-                  dim3(256), (uint32_t)((size_t)K * H * 4), E, stride, routing, weights, hbuf, K, D, x_inout,
-                  moe_out);
+    const dim3 g((unsigned)((D + 4 * RW - 1) / (4 * RW)), (unsigned)T), b(256);
+    const uint32_t lds = (uint32_t)((size_t)K * H * 4);
+    const int per = (K * H / 4 + 255) / 256;  // h units per thread
+    if (per <= 4)
+        return launch(L, down_fast_kernel<DT, NH, RW, 4>, g, b, lds, E, stride, routing, weights, hbuf, K, D, x_inout,
+                      moe_out);
+    if (per <= 8)
+        return launch(L, down_fast_kernel<DT, NH, RW, 8>, g, b, lds, E, stride, routing, weights, hbuf, K, D, x_inout,
+                      moe_out);
+    return launch(L, down_fast_kernel<DT, NH, RW, kHStageMax>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
+                  x_inout, moe_out);
 }
 
 template <int DT>
@@ -362,7 +393,7 @@ bool experts_decode_supported(int dtype, int T, int K, int D, int H, const void 
     const int nc = D / step, nh = H / step;
     const bool nc_ok = D % step == 0 && (nc == 1 || nc == 2 || nc == 3 || nc == 4 || nc == 6 || nc == 8);
     const bool nh_ok = H % step == 0 && nh >= 1 && nh <= 4;
-    return nc_ok && nh_ok && H % 2 == 0 && T >= 1 && T <= 65535 && (size_t)K * H * 4 <= 64 * 1024 &&
+    return nc_ok && nh_ok && H % 2 == 0 && T >= 1 && T <= 65535 && (size_t)K * H <= 4 * 256 * kHStageMax &&
            aligned16(experts) && stride % 16 == 0 && aligned16(xb) && aligned16(hbuf);
 }
 
