@@ -185,6 +185,129 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 
 }
 
+// Few tokens (decode), AVX2 order, bf16 weights, D a multiple of 128: one 64-thread block per 4 router
+// rows of one token, thread (row rr, chain c). Chain c's operands are staged transposed in LDS --
+// wt[rr][c][m] = W[r][16m + c], xt[c][m] = x[16m + c] -- so a 16-byte read carries 8 steps of one
+// chain (48 reads for 128 steps instead of 256 narrow ones) and the chain's dependent adds are the
+// only long pole. Staging: a thread takes 8 consecutive steps of 8 chains (eight 16-byte loads of
+// the row) and transposes them in registers (v_perm pairs the 16-bit halves) into eight 16-byte
+// LDS stores. The 16 chains of a row sit in 16 consecutive lanes: (chain j) + (chain 8+j) via a
+// DPP row rotation, then the sequential sum over j, as the engine's lanes a[j] + b[j].
+constexpr int kDRows = 4;
+template <int M>  // steps per chain = D / 16, a multiple of 8
+__global__ __launch_bounds__(64) void router_decode_kernel(const float *__restrict__ xb, const uint16_t *__restrict__ W,
+                                                          const float *__restrict__ bias, int E,
+                                                          float *__restrict__ logits) {
+    constexpr int D = 16 * M;
+    constexpr int WP = M + 8;  // bf16 per (row, chain) line: 16-byte pad, lanes of one read hit distinct banks
+    constexpr int XP = M + 4;  // f32 per chain line
+    constexpr int G = M / 8;   // 8-step groups per chain
+    __shared__ __align__(16) uint16_t wt[kDRows * 16 * WP];
+    __shared__ __align__(16) float xt[16 * XP];
+    const int tid = threadIdx.x, rr = tid >> 4, c = tid & 15;
+    const int t = blockIdx.y, r0 = blockIdx.x * kDRows;
+    const float *x = xb + (size_t)t * D;
+
+    // ---- staging tasks: (row, half h, group g) for W, (half h, group g) for x; all loads first
+    constexpr int WT = kDRows * 2 * G, XT = 2 * G;
+    constexpr int WPER = (WT + 63) / 64, XPER = (XT + 63) / 64;
+    u32x4 wv[WPER][8];
+    f32x4 xv[XPER][8][2];
+#pragma unroll
+    for (int q = 0; q < WPER; ++q) {
+        const int task = min(tid + 64 * q, WT - 1);
+        const int row = task / (2 * G), h = (task / G) & 1, g = task % G;
+        const int r = min(r0 + row, E - 1);
+        const uint16_t *src = W + (size_t)r * D + 8 * h;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv[q][i] = *reinterpret_cast<const u32x4 *>(src + 16 * (8 * g + i));
+    }
+#pragma unroll
+    for (int q = 0; q < XPER; ++q) {
+        const int task = min(tid + 64 * q, XT - 1);
+        const int h = task / G, g = task % G;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float *src = x + 16 * (8 * g + i) + 8 * h;
+            xv[q][i][0] = *reinterpret_cast<const f32x4 *>(src);
+            xv[q][i][1] = *reinterpret_cast<const f32x4 *>(src + 4);
+        }
+    }
+    // transposed stores (clamped tasks rewrite the last task's identical data)
+#pragma unroll
+    for (int q = 0; q < WPER; ++q) {
+        const int task = min(tid + 64 * q, WT - 1);
+        const int row = task / (2 * G), h = (task / G) & 1, g = task % G;
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) {
+            // chain 8h+ch, steps 8g..8g+7: bf16 #ch of units i = 0..7; dword k packs units 2k, 2k+1
+            uint32_t d[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t a = wv[q][2 * k][ch >> 1], b = wv[q][2 * k + 1][ch >> 1];
+                // low half = unit 2k's bf16, high half = unit 2k+1's; ch odd selects the high halves
+                d[k] = (ch & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
+            }
+            *reinterpret_cast<u32x4 *>(&wt[(row * 16 + 8 * h + ch) * WP + 8 * g]) = u32x4{d[0], d[1], d[2], d[3]};
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < XPER; ++q) {
+        const int task = min(tid + 64 * q, XT - 1);
+        const int h = task / G, g = task % G;
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) {
+            f32x4 lo, hi;
+            lo.x = xv[q][0][ch >> 2][ch & 3]; lo.y = xv[q][1][ch >> 2][ch & 3];
+            lo.z = xv[q][2][ch >> 2][ch & 3]; lo.w = xv[q][3][ch >> 2][ch & 3];
+            hi.x = xv[q][4][ch >> 2][ch & 3]; hi.y = xv[q][5][ch >> 2][ch & 3];
+            hi.z = xv[q][6][ch >> 2][ch & 3]; hi.w = xv[q][7][ch >> 2][ch & 3];
+            float *dst = &xt[(8 * h + ch) * XP + 8 * g];
+            *reinterpret_cast<f32x4 *>(dst) = lo;
+            *reinterpret_cast<f32x4 *>(dst + 4) = hi;
+        }
+    }
+    __syncthreads();
+
+    // ---- chain c of row rr, 128 steps in column order (rounded product, then add)
+    const uint16_t *wl = &wt[(rr * 16 + c) * WP];
+    const float *xl = &xt[c * XP];
+    float acc = 0.0f;
+#pragma unroll 4
+    for (int g = 0; g < G; ++g) {
+        const u32x4 w8 = *reinterpret_cast<const u32x4 *>(wl + 8 * g);
+        const f32x4 xa = *reinterpret_cast<const f32x4 *>(xl + 8 * g);
+        const f32x4 xc = *reinterpret_cast<const f32x4 *>(xl + 8 * g + 4);
+        acc = acc + bf16_lo(w8.x) * xa.x;
+        acc = acc + bf16_hi(w8.x) * xa.y;
+        acc = acc + bf16_lo(w8.y) * xa.z;
+        acc = acc + bf16_hi(w8.y) * xa.w;
+        acc = acc + bf16_lo(w8.z) * xc.x;
+        acc = acc + bf16_hi(w8.z) * xc.y;
+        acc = acc + bf16_lo(w8.w) * xc.z;
+        acc = acc + bf16_hi(w8.w) * xc.w;
+    }
+    // lanes c and c+8 of the row: row_ror:8 brings chain c+8 to lane c
+    const float other = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x128, 0xF, 0xF, false));
+    const float pair = acc + other;  // lanes c < 8: a[c] + b[c]
+    float rs[kDRows];  // each row's sum over j, in order, from wave-uniform lanes
+#pragma unroll
+    for (int R = 0; R < kDRows; ++R) {
+        rs[R] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rs[R] = rs[R] + lane_value(pair, 16 * R + j);
+    }
+    float sum = rs[0];
+#pragma unroll
+    for (int R = 1; R < kDRows; ++R) sum = rr == R ? rs[R] : sum;
+    const int r = r0 + rr;
+    if (c == 0 && r < E) {
+        if (bias) sum = sum + bias[r];
+        logits[(size_t)t * E + r] = sum;
+    }
+}
+
 // Many tokens, AVX2 order: the router tile is shared by a block's tokens instead of re-read per token.
 // grid (ceil(E/16), ceil(T/8)), 256 threads: tid -> half h = tid & 1, router row 16*bx + ((tid >> 1) & 15),
 // token 8*by + (tid >> 5). Thread (t, r, h) runs chains 8h..8h+7 of row r for token t: step m adds the
@@ -417,6 +540,33 @@ hipError_t launch_logits(const Launch &L, const float *xb, const void *W, const 
                   (uint32_t)lds, xb, W, bias, E, D, rpb, vec ? 1 : 0, probs);
 }
 
+// The decode kernel (AVX2 order, bf16) below 16 tokens, for the row lengths instantiated below.
+inline bool decode_ok(int T, int D, int dtype, const void *W, const float *xb) {
+    const int m = D / 16;
+    const bool m_ok = D % 16 == 0 && (m == 8 || m == 16 || m == 32 || m == 48 || m == 64 || m == 96 || m == 128 ||
+                                      m == 192 || m == 256);
+    return T < 16 && dtype == RBT_DT_BF16 && m_ok && (reinterpret_cast<uintptr_t>(W) % 16 == 0) &&
+           (reinterpret_cast<uintptr_t>(xb) % 16 == 0);
+}
+
+inline hipError_t launch_router_decode(const Launch &L, const float *xb, const void *W, const float *bias, int T, int E,
+                                       int D, float *logits) {
+    const dim3 g((unsigned)((E + kDRows - 1) / kDRows), (unsigned)T), b(64);
+    const uint16_t *w = static_cast<const uint16_t *>(W);
+    switch (D / 16) {
+        case 8: return launch(L, router_decode_kernel<8>, g, b, 0, xb, w, bias, E, logits);
+        case 16: return launch(L, router_decode_kernel<16>, g, b, 0, xb, w, bias, E, logits);
+        case 32: return launch(L, router_decode_kernel<32>, g, b, 0, xb, w, bias, E, logits);
+        case 48: return launch(L, router_decode_kernel<48>, g, b, 0, xb, w, bias, E, logits);
+        case 64: return launch(L, router_decode_kernel<64>, g, b, 0, xb, w, bias, E, logits);
+        case 96: return launch(L, router_decode_kernel<96>, g, b, 0, xb, w, bias, E, logits);
+        case 128: return launch(L, router_decode_kernel<128>, g, b, 0, xb, w, bias, E, logits);
+        case 192: return launch(L, router_decode_kernel<192>, g, b, 0, xb, w, bias, E, logits);
+        case 256: return launch(L, router_decode_kernel<256>, g, b, 0, xb, w, bias, E, logits);
+        default: return hipErrorNotSupported;
+    }
+}
+
 // The batch kernel (AVX2 order) from 16 tokens on; its 16-byte staging needs 16-byte aligned rows.
 inline bool batch_ok(int T, int D, int dtype, const void *W, const float *xb) {
     const int esz = dtype == RBT_DT_BF16 ? 2 : 4;
@@ -428,7 +578,9 @@ template <int NCH, int DT>
 hipError_t launch_t(const Launch &L, const Launch &Lk, const float *xb, const void *W, const float *bias, int T, int E,
                     int D, int K, int norm_topk, float *probs, int32_t *routing, float *weights) {
     hipError_t e;
-    if (NCH == 16 && batch_ok(T, D, DT, W, xb)) {
+    if (NCH == 16 && decode_ok(T, D, DT, W, xb)) {
+        e = launch_router_decode(L, xb, W, bias, T, E, D, probs);
+    } else if (NCH == 16 && batch_ok(T, D, DT, W, xb)) {
         e = launch(L, router_logits_batch_kernel<DT>, dim3((E + kBRows - 1) / kBRows, (T + kBTok - 1) / kBTok),
                    dim3(256), 0, xb, W, bias, T, E, D, probs);
     } else {
@@ -453,6 +605,7 @@ hipError_t launch_router_logits(const Launch &L, int order, int dtype, const flo
     if (T <= 0) return hipSuccess;
     if (T > 65535) return hipErrorInvalidValue;
     if (order == RBT_ORDER_AVX2) {
+        if (decode_ok(T, D, dtype, W, xb)) return launch_router_decode(L, xb, W, bias, T, E, D, logits);
         if (batch_ok(T, D, dtype, W, xb))
             return dtype == RBT_DT_BF16
                        ? launch(L, router_logits_batch_kernel<RBT_DT_BF16>,
