@@ -364,18 +364,35 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
                                         moe_dev, w.probs, L->n_experts, L->norm_topk));
         return prof_collect(h);
     }
-    HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
-                            L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
-                            weights));
     if (prefill_supported(L->dtype, T, h->prefill_min_tokens, L->n_experts, L->top_k, L->dim, L->expert_hidden,
                           L->experts, L->expert_stride, xb_dev)) {
         if (!pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim))) return 0;
+        // router, top-k and the activation split in one launch when it applies, else the two router
+        // kernels (the grouped path then splits the activations itself)
+        const bool fused = router_prefill_supported(h->order, L->dtype, T, L->n_experts, L->dim, L->top_k,
+                                                    L->router, xb_dev);
+        if (fused) {
+            uint16_t *x_hi = nullptr, *x_lo = nullptr;
+            prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
+            HIP_OK(h, launch_router_prefill(lc(h, kProfRouter), L->dtype, xb_dev, L->router, L->router_bias, T,
+                                            L->n_experts, L->dim, L->top_k, L->norm_topk, routing, weights, x_hi,
+                                            x_lo));
+        } else {
+            HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
+                                    L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs,
+                                    routing, weights));
+        }
         int32_t *counts = nullptr;
         HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
                                  L->experts, L->expert_stride, xb_dev, T, L->n_experts, L->top_k, L->dim,
-                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts));
+                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts, fused));
         h->expert_counts = counts;
-    } else if (decode_kernels) {
+        return prof_collect(h);
+    }
+    HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
+                            L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
+                            weights));
+    if (decode_kernels) {
         HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
                                         routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
                                         moe_dev, nullptr, L->n_experts, L->norm_topk));

@@ -45,83 +45,94 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
 // routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);
 // perm[P]: pair ids grouped by expert, increasing within an expert; pos_of[P]: inverse of perm;
 // m_off[E+1]: exclusive prefix of ceil(counts / 64).
+// Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
+// equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
+// row; a pair's rank inside its wave's slice goes to pos_of as a temporary. B: wave 0 (4 experts per
+// lane) sums the waves' counts, scans them into the offsets, and turns each wave's counts into that
+// wave's first position per expert. C: every pair adds its wave's base. Three barriers in all.
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ routing, int P, int E,
                                                         int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ perm, int32_t *__restrict__ pos_of,
                                                         int32_t *__restrict__ m_off) {
-    __shared__ int s_cnt[kDispatchMaxE];
-    __shared__ int s_off[kDispatchMaxE];
-    __shared__ int s_run[kDispatchMaxE];
-    __shared__ int s_w[16][kDispatchMaxE];  // per-wave counts of the current chunk
-    __shared__ int s_scan[1024];
+    constexpr int NW = 16;
+    __shared__ int s_w[NW][kDispatchMaxE];  // A: running counts per wave; B: each wave's base positions
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int e = tid; e < E; e += 1024) {
-        s_cnt[e] = 0;
-        s_run[e] = 0;
-    }
+    for (int i = tid; i < NW * kDispatchMaxE; i += 1024) (&s_w[0][0])[i] = 0;
     __syncthreads();
-    for (int p = tid; p < P; p += 1024) {
-        const int r = routing[p];
-        atomicAdd(&s_cnt[min(max(r, 0), E - 1)], 1);
-    }
-    __syncthreads();
-    // exclusive scans of the counts (pass 0) and of the tile counts (pass 1), Hillis-Steele
-    for (int pass = 0; pass < 2; ++pass) {
-        int v = 0;
-        if (tid < E) v = pass == 0 ? s_cnt[tid] : (s_cnt[tid] + kMT - 1) / kMT;
-        s_scan[tid] = v;
-        __syncthreads();
-        for (int o = 1; o < 1024; o <<= 1) {
-            const int add = tid >= o ? s_scan[tid - o] : 0;
-            __syncthreads();
-            s_scan[tid] += add;
-            __syncthreads();
-        }
-        const int incl = s_scan[tid];
-        int32_t *dst = pass == 0 ? offsets : m_off;
-        if (tid < E) {
-            dst[tid] = incl - v;
-            if (pass == 0) {
-                s_off[tid] = incl - v;
-                counts[tid] = v;
-            }
-        }
-        if (tid == E - 1) dst[E] = incl;
-        __syncthreads();
-    }
-    // stable placement, 1024 pairs at a time; rank within the wave from ballots over the expert bits
+    const int S = ((P + NW - 1) / NW + 63) / 64 * 64;  // slice per wave, whole 64-pair steps
+    const int base = wv * S, end = min(P, base + S);
     const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int c0 = 0; c0 < P; c0 += 1024) {
-        for (int i = tid; i < 16 * kDispatchMaxE; i += 1024) (&s_w[0][0])[i] = 0;
-        __syncthreads();
-        const int p = c0 + tid;
-        const bool valid = p < P;
+    for (int p0 = base; p0 < end; p0 += 64) {  // wave-uniform loop
+        const int p = p0 + lane;
+        const bool valid = p < end;
         const int e = valid ? min(max(routing[p], 0), E - 1) : 0;
         uint64_t same = __ballot(valid);
+#pragma unroll
         for (int b = 0; b < 8; ++b) {
             const bool bit = (e >> b) & 1;
             const uint64_t ones = __ballot(bit);
             same &= bit ? ones : ~ones;
         }
         const int before = __popcll(same & below);
-        if (valid && (same >> lane) == 1ull) s_w[wv][e] = before + 1;  // last lane of its expert
-        __syncthreads();
-        int pos = 0;
-        if (valid) {
-            pos = s_off[e] + s_run[e] + before;
-            for (int w = 0; w < wv; ++w) pos += s_w[w][e];
-        }
-        __syncthreads();
-        if (tid < E) {
+        const int cur = valid ? s_w[wv][e] : 0;  // read by every lane before any update (in-order LDS)
+        if (valid) pos_of[p] = cur + before;
+        if (valid && (same >> lane) == 1ull) s_w[wv][e] = cur + before + 1;  // last lane of its expert
+    }
+    __syncthreads();
+    if (wv == 0) {
+        int c[4], mt[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
             int tot = 0;
-            for (int w = 0; w < 16; ++w) tot += s_w[w][tid];
-            s_run[tid] += tot;
+            if (e < E)
+                for (int w = 0; w < NW; ++w) tot += s_w[w][e];
+            c[i] = tot;
+            mt[i] = (tot + kMT - 1) / kMT;
         }
-        if (valid) {
+        // exclusive scans across the wave of the lanes' sums (4 experts per lane, ascending)
+        int sc = ((c[0] + c[1]) + c[2]) + c[3], sm = ((mt[0] + mt[1]) + mt[2]) + mt[3];
+        int ic = sc, im = sm;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int uc = __shfl_up(ic, d, 64), um = __shfl_up(im, d, 64);
+            if (lane >= d) {
+                ic += uc;
+                im += um;
+            }
+        }
+        int oc = ic - sc, om = im - sm;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
+            if (e < E) {
+                counts[e] = c[i];
+                offsets[e] = oc;
+                m_off[e] = om;
+                int run = oc;  // each wave's first position for expert e
+                for (int w = 0; w < NW; ++w) {
+                    const int n = s_w[w][e];
+                    s_w[w][e] = run;
+                    run += n;
+                }
+            }
+            if (e == E - 1) {
+                offsets[E] = oc + c[i];
+                m_off[E] = om + mt[i];
+            }
+            oc += c[i];
+            om += mt[i];
+        }
+    }
+    __syncthreads();
+    for (int p0 = base; p0 < end; p0 += 64) {
+        const int p = p0 + lane;
+        if (p < end) {
+            const int e = min(max(routing[p], 0), E - 1);
+            const int pos = s_w[wv][e] + pos_of[p];
             perm[pos] = p;
             pos_of[p] = pos;
         }
-        __syncthreads();
     }
 }
 
@@ -372,10 +383,14 @@ size_t prefill_workspace_bytes(int T, int E, int K, int D) {
            2 * up(2 * (size_t)T * D);
 }
 
-hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
-                          uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
-                          const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
-                          int32_t **counts_out) {
+namespace {
+// Workspace carve-up of the grouped path (prefill_workspace_bytes is its total).
+struct PrefillWs {
+    int32_t *counts, *offsets, *m_off, *perm, *pos_of;
+    float *y;
+    uint16_t *x_hi, *x_lo;
+};
+PrefillWs carve_ws(void *ws, int T, int E, int K, int D) {
     const int P = T * K;
     uint8_t *w = static_cast<uint8_t *>(ws);
     auto carve = [&](size_t bytes) {
@@ -383,25 +398,50 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
         w += (bytes + 255) / 256 * 256;
         return p;
     };
-    int32_t *counts = reinterpret_cast<int32_t *>(carve(4 * (size_t)E));
-    int32_t *offsets = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
-    int32_t *m_off = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
-    int32_t *perm = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
-    int32_t *pos_of = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
-    float *y = reinterpret_cast<float *>(carve(4 * (size_t)P * D));
-    uint16_t *x_hi = reinterpret_cast<uint16_t *>(carve(2 * (size_t)T * D));
-    uint16_t *x_lo = reinterpret_cast<uint16_t *>(carve(2 * (size_t)T * D));
+    PrefillWs r;
+    r.counts = reinterpret_cast<int32_t *>(carve(4 * (size_t)E));
+    r.offsets = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
+    r.m_off = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
+    r.perm = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
+    r.pos_of = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
+    r.y = reinterpret_cast<float *>(carve(4 * (size_t)P * D));
+    r.x_hi = reinterpret_cast<uint16_t *>(carve(2 * (size_t)T * D));
+    r.x_lo = reinterpret_cast<uint16_t *>(carve(2 * (size_t)T * D));
+    return r;
+}
+}  // namespace
+
+void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uint16_t **x_lo) {
+    const PrefillWs r = carve_ws(ws, T, E, K, D);
+    *x_hi = r.x_hi;
+    *x_lo = r.x_lo;
+}
+
+hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
+                          uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
+                          const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
+                          int32_t **counts_out, bool x_split_done) {
+    const int P = T * K;
+    const PrefillWs r = carve_ws(ws, T, E, K, D);
+    int32_t *counts = r.counts, *offsets = r.offsets, *m_off = r.m_off, *perm = r.perm, *pos_of = r.pos_of;
+    float *y = r.y;
+    uint16_t *x_hi = r.x_hi, *x_lo = r.x_lo;
     // the h planes (bf16 hi, lo; [P][H] each) take the f32 [P][H] h buffer
     uint16_t *h_hi = reinterpret_cast<uint16_t *>(hbuf), *h_lo = h_hi + (size_t)P * H;
     if (counts_out) *counts_out = counts;
-    // activation split, then the dispatch: one timed interval (split start .. dispatch end)
-    Launch Ls = Ld, Ldd = Ld;
-    Ls.stop = nullptr;
-    Ldd.start = nullptr;
-    const size_t n8 = (size_t)T * D / 8;
-    const unsigned sblocks = (unsigned)std::min<size_t>((n8 + 255) / 256, 2048);
-    hipError_t e = launch(Ls, split_hilo_kernel, dim3(sblocks), dim3(256), 0, xb, n8, x_hi, x_lo);
-    if (e != hipSuccess) return e;
+    // activation split (unless the router kernel wrote the planes), then the dispatch: one timed
+    // interval (first start .. dispatch end)
+    hipError_t e = hipSuccess;
+    Launch Ldd = Ld;
+    if (!x_split_done) {
+        Launch Ls = Ld;
+        Ls.stop = nullptr;
+        Ldd.start = nullptr;
+        const size_t n8 = (size_t)T * D / 8;
+        const unsigned sblocks = (unsigned)std::min<size_t>((n8 + 255) / 256, 2048);
+        e = launch(Ls, split_hilo_kernel, dim3(sblocks), dim3(256), 0, xb, n8, x_hi, x_lo);
+        if (e != hipSuccess) return e;
+    }
     e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off);
     if (e != hipSuccess) return e;
     const uint8_t *ex = static_cast<const uint8_t *>(experts);

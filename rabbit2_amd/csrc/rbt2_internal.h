@@ -130,10 +130,20 @@ constexpr int kPrefillMinTokensDefault = 12;  // measured crossover with the per
 bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, int H, const void *experts,
                        uint64_t stride, const float *xb);
 size_t prefill_workspace_bytes(int T, int E, int K, int D);
+// x_split_done: the bf16 hi/lo planes of xb are already in the workspace (prefill_x_planes), written
+// by launch_router_prefill.
 hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
-                          int32_t **counts_out);
+                          int32_t **counts_out, bool x_split_done);
+void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uint16_t **x_lo);
+
+// Router logits + softmax + top-k + the activation hi/lo split in one launch, for the grouped path
+// (AVX2 order, E <= 64). x_hi/x_lo may be NULL (no split).
+bool router_prefill_supported(int order, int dtype, int T, int E, int D, int K, const void *W, const float *xb);
+hipError_t launch_router_prefill(const Launch &L, int dtype, const float *xb, const void *W, const float *bias, int T,
+                                 int E, int D, int K, int norm_topk, int32_t *routing, float *weights,
+                                 uint16_t *x_hi, uint16_t *x_lo);
 
 // Dense matvec (one row per wave).
 hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);

@@ -308,6 +308,193 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
     }
 }
 
+// Softmax + top-k of one token's E <= 64 logits by one wave (lane = expert), the engine's arithmetic
+// (rabbit2.c:399-405 softmax with max-subtract, exp, sequential sum, divide; :516-528 K rounds of
+// "largest unused, lowest index on ties" = the first K places of a stable descending sort; :539
+// norm_topk). s_v: this wave's 64-float LDS scratch. NaN: as the engine's '>' scans (a NaN logit
+// never wins a comparison, except that element 0 starts the max scan).
+__device__ __forceinline__ void wave_softmax_topk(float v, int E, int K, int norm_topk, float *s_v, float *s_p,
+                                                  int32_t *routing_t, float *weights_t) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if (lane >= E) v = -INFINITY;
+    float mx = wave_max(v);
+    const float first = lane_value(v, 0);
+    if (first != first) mx = first;
+    const float e = lane < E ? (float)exp((double)(v - mx)) : 0.0f;
+    s_v[lane] = e;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const f32x4 *p4 = reinterpret_cast<const f32x4 *>(s_v);
+    float sum = 0.0f;  // every lane, sequentially in the engine's order (entries past E are 0, last)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const f32x4 v4 = p4[q];
+        sum = sum + v4.x;
+        sum = sum + v4.y;
+        sum = sum + v4.z;
+        sum = sum + v4.w;
+    }
+    const float p = e / sum;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    s_v[lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int rank;
+    if (sum != sum) {
+        rank = lane;  // all NaN: each round keeps the first unused index
+    } else {
+        int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const f32x4 v4 = p4[q];
+            const int j = 4 * q;
+            r0 += (v4.x > p) | ((v4.x == p) & (j < lane));
+            r1 += (v4.y > p) | ((v4.y == p) & (j + 1 < lane));
+            r2 += (v4.z > p) | ((v4.z == p) & (j + 2 < lane));
+            r3 += (v4.w > p) | ((v4.w == p) & (j + 3 < lane));
+        }
+        rank = (r0 + r1) + (r2 + r3);
+    }
+    if (lane < E && rank < K) {
+        routing_t[rank] = lane;
+        s_p[rank] = p;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float wsum = 0.0f;
+    for (int k = 0; k < K; ++k) wsum = wsum + s_p[k];
+    if (lane < K) weights_t[lane] = norm_topk ? s_p[lane] / wsum : s_p[lane];
+}
+
+// Prefill front end in one launch (AVX2 order, E <= 64, bf16): router logits, softmax + top-k, and the
+// bf16 hi/lo split of x for the grouped GEMMs. One block per kPTok tokens covers all router rows, so the
+// top-k runs in the block. Wave (token tl, half h) holds the 64 router rows in its lanes and runs
+// chains 8h..8h+7 of each (as the batched kernel); x is then the same for the whole wave, so it is read
+// with scalar loads and enters the multiplies as a scalar operand, and LDS only serves the router rows
+// (one 16-byte read per step and lane). Router columns stream through LDS in double-buffered chunks of
+// kPCols; each x element's hi/lo parts are written by one thread.
+constexpr int kPTok = 2, kPCols = 512, kPThreads = kPTok * 64 * 2;
+template <int DT>
+__global__ __launch_bounds__(kPThreads) void router_prefill_kernel(const float *__restrict__ xb,
+                                                                   const void *__restrict__ Wv,
+                                                                   const float *__restrict__ bias, int T, int E, int D,
+                                                                   int K, int norm_topk, int32_t *__restrict__ routing,
+                                                                   float *__restrict__ weights,
+                                                                   uint16_t *__restrict__ x_hi,
+                                                                   uint16_t *__restrict__ x_lo) {
+    static_assert(DT == RBT_DT_BF16, "bf16 router rows");
+    constexpr int CW = kPCols;          // columns per chunk (1 KiB per row)
+    constexpr int WP = CW * 2 + 32;     // row pitch in bytes (16-byte reads of 16 consecutive rows hit distinct banks)
+    constexpr int UPR = CW * 2 / 16;    // 16-byte units per row per chunk
+    constexpr int WU = 64 * UPR / kPThreads;  // per thread per chunk
+    __shared__ __align__(16) unsigned char wt[2][64 * WP];
+    __shared__ __align__(16) float s_part[kPTok][8][64];  // chains 8..15 of each (token, row)
+    __shared__ __align__(16) float s_log[kPTok][64];
+    __shared__ __align__(16) float s_v[kPTok][64];
+    __shared__ float s_p[kPTok][64];
+    const uint16_t *Wg = static_cast<const uint16_t *>(Wv);
+    const int tid = threadIdx.x, r = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int h = wv & 1, tl = wv >> 1;
+    const int t0 = blockIdx.x * kPTok;
+    const int ntok = min(kPTok, T - t0);
+    const int body = (D / 16) * 16;
+    const int nch = (body + CW - 1) / CW;
+    const bool live = tl < ntok;  // wave-uniform
+    const float *xrow = xb + (size_t)(t0 + (live ? tl : 0)) * D + 8 * h;
+
+    u32x4 wv4[WU];
+    auto load = [&](int c) {
+        const int c0 = c * CW, upr = min(CW, body - c0) / 8;
+#pragma unroll
+        for (int i = 0; i < WU; ++i) {
+            const int u = tid + i * kPThreads, row = u / UPR, k = min(u % UPR, upr - 1);
+            wv4[i] = *reinterpret_cast<const u32x4 *>(Wg + (size_t)min(row, E - 1) * D + c0 + 8 * k);
+        }
+    };
+    auto store = [&](int c) {
+        const int upr = min(CW, body - c * CW) / 8;
+#pragma unroll
+        for (int i = 0; i < WU; ++i) {
+            const int u = tid + i * kPThreads, row = u / UPR, k = min(u % UPR, upr - 1);
+            *reinterpret_cast<u32x4 *>(wt[c & 1] + row * WP + k * 16) = wv4[i];
+        }
+    };
+
+    // the hi/lo split of this block's x rows: plain loads and stores, one 16-byte unit per thread step
+    if (x_hi) {
+        const int units = ntok * D / 4;
+        for (int u = tid; u < units; u += kPThreads) {
+            const int tt = u / (D / 4), k = u % (D / 4);
+            const size_t o = (size_t)(t0 + tt) * D + 4 * k;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(xb + o);
+            uint32_t hb[4], lb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t q = __float_as_uint(v[j]);
+                q += 0x7FFFu + ((q >> 16) & 1u);
+                hb[j] = q >> 16;
+                uint32_t l = __float_as_uint(v[j] - __uint_as_float(hb[j] << 16));
+                l += 0x7FFFu + ((l >> 16) & 1u);
+                lb[j] = l >> 16;
+            }
+            *reinterpret_cast<uint2 *>(x_hi + o) = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+            *reinterpret_cast<uint2 *>(x_lo + o) = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+        }
+    }
+
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    if (nch > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+        const bool more = c + 1 < nch;
+        if (more) load(c + 1);  // in flight during this chunk's chains
+        const int c0 = c * CW, steps = min(CW, body - c0) / 16;
+        if (live && r < E) {
+            const unsigned char *wr = wt[c & 1] + r * WP + 16 * h;
+            const float *xc = xrow + c0;
+#pragma unroll 8
+            for (int m = 0; m < steps; ++m) {
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(wr + 32 * m);
+                const float *xs = xc + 16 * m;  // wave-uniform: scalar loads
+                acc[0] = acc[0] + bf16_lo(a.x) * xs[0];
+                acc[1] = acc[1] + bf16_hi(a.x) * xs[1];
+                acc[2] = acc[2] + bf16_lo(a.y) * xs[2];
+                acc[3] = acc[3] + bf16_hi(a.y) * xs[3];
+                acc[4] = acc[4] + bf16_lo(a.z) * xs[4];
+                acc[5] = acc[5] + bf16_hi(a.z) * xs[5];
+                acc[6] = acc[6] + bf16_lo(a.w) * xs[6];
+                acc[7] = acc[7] + bf16_hi(a.w) * xs[7];
+            }
+        }
+        if (more) store(c + 1);  // the other buffer: last read in chunk c-1, before the barrier below
+        __syncthreads();
+    }
+    if (h == 1 && live) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s_part[tl][j][r] = acc[j];
+    }
+    __syncthreads();
+    if (h == 0 && live && r < E) {
+        float sum = 0.0f;  // the engine's lanes a[j] + b[j], summed from j = 0
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum = sum + (acc[j] + s_part[tl][j][r]);
+        const uint16_t *wrow = Wg + (size_t)r * D;
+        const float *x = xb + (size_t)(t0 + tl) * D;
+        for (int i = body; i < D; ++i) sum = sum + widen<DT>(wrow[i]) * x[i];
+        if (bias) sum = sum + bias[r];
+        s_log[tl][r] = sum;
+    }
+    __syncthreads();
+    if (wv < ntok) {
+        const int lane = tid & 63;
+        wave_softmax_topk(lane < E ? s_log[wv][lane] : 0.0f, E, K, norm_topk, s_v[wv], s_p[wv],
+                          routing + (size_t)(t0 + wv) * K, weights + (size_t)(t0 + wv) * K);
+    }
+}
+
 // Many tokens, AVX2 order: the router tile is shared by a block's tokens instead of re-read per token.
 // grid (ceil(E/16), ceil(T/8)), 256 threads: tid -> half h = tid & 1, router row 16*bx + ((tid >> 1) & 15),
 // token 8*by + (tid >> 5). Thread (t, r, h) runs chains 8h..8h+7 of row r for token t: step m adds the
@@ -623,6 +810,21 @@ hipError_t launch_router_logits(const Launch &L, int order, int dtype, const flo
     }
     return dtype == RBT_DT_BF16 ? launch_logits<4, RBT_DT_BF16, false>(L, xb, W, bias, T, E, D, 64, logits)
                                 : launch_logits<4, RBT_DT_F32, false>(L, xb, W, bias, T, E, D, 64, logits);
+}
+
+bool router_prefill_supported(int order, int dtype, int T, int E, int D, int K, const void *W, const float *xb) {
+    return order == RBT_ORDER_AVX2 && dtype == RBT_DT_BF16 && T >= 1 && E >= 1 && E <= 64 && K <= E && D >= 16 &&
+           D % 8 == 0 && (reinterpret_cast<uintptr_t>(W) % 16 == 0) && (reinterpret_cast<uintptr_t>(xb) % 16 == 0);
+}
+
+hipError_t launch_router_prefill(const Launch &L, int dtype, const float *xb, const void *W, const float *bias, int T,
+                                 int E, int D, int K, int norm_topk, int32_t *routing, float *weights,
+                                 uint16_t *x_hi, uint16_t *x_lo) {
+    if (T <= 0) return hipSuccess;
+    if (dtype != RBT_DT_BF16) return hipErrorNotSupported;  // the grouped path is bf16 only
+    const dim3 g((unsigned)((T + kPTok - 1) / kPTok)), b(kPThreads);
+    return launch(L, router_prefill_kernel<RBT_DT_BF16>, g, b, 0, xb, W, bias, T, E, D, K, norm_topk, routing, weights,
+                  x_hi, x_lo);
 }
 
 hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype, const float *xb, const void *W,

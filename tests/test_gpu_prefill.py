@@ -57,6 +57,7 @@ GROUPED_SHAPES = [
     (1024, 64, 8, 128, 1, 17),   # E 64, K 8 with 17 tokens: many experts with 1-3 rows
     (768, 256, 6, 384, 0, 33),   # E 256 (the dispatch maximum), H 384
     (2048, 64, 8, 1024, 1, 100),  # OLMoE layer, 800 pairs: ~12 rows per expert
+    (768, 64, 8, 256, 0, 21),    # E <= 64: one-launch router + top-k, 768 = a full and a half column chunk
 ]
 
 
