@@ -335,7 +335,27 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
         for _ in range(reps):
             dev.moe_dev(L, xb, T, moe=moe)
         hipapi.hipEventRecord(e1, stream)
+        us_eager = 1000.0 * elapsed(e0, e1) / reps
+        # the same call captured as a HIP graph (kernels only), checked against the eager output
+        dev.synchronize()
+        eager_out = dev.d2h(moe, (T, D), np.float32)
+        graph, gexec = C.c_void_p(), C.c_void_p()
+        assert hipapi.hipStreamBeginCapture(stream, 2) == 0
+        dev.moe_dev(L, xb, T, moe=moe)
+        assert hipapi.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        assert hipapi.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0) == 0
+        for _ in range(3):
+            dev.memset(moe, 0)
+            assert hipapi.hipGraphLaunch(gexec, stream) == 0
+            dev.synchronize()
+            assert dev.d2h(moe, (T, D), np.float32).tobytes() == eager_out.tobytes(), "prefill graph replay differs"
+        hipapi.hipEventRecord(e0, stream)
+        for _ in range(reps):
+            hipapi.hipGraphLaunch(gexec, stream)
+        hipapi.hipEventRecord(e1, stream)
         us = 1000.0 * elapsed(e0, e1) / reps
+        hipapi.hipGraphExecDestroy(gexec)
+        hipapi.hipGraphDestroy(graph)
         dev.profile(True)
         for _ in range(reps):
             dev.moe_dev(L, xb, T, moe=moe)
@@ -358,6 +378,7 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
                 kern[kname]["weight_GBps"] = round(wbytes / t / 1e9, 1)
         res[name] = {
             "us_per_call": round(us, 2),
+            "us_per_call_eager": round(us_eager, 2),
             "tok_per_s": round(T / (us * 1e-6), 1),
             "hbm_GBps_alg": round(alg_bytes / (us * 1e-6) / 1e9, 1),
             "hbm_frac_alg": round(alg_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -367,7 +388,8 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             "row_tiles": tiles,
         }
     out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,
-           "note": "per-call time of the whole MoE block (router .. combine), eager launches, inputs in HBM",
+           "note": "per-call time of the whole MoE block (router .. combine), HIP graph replay of one call "
+                   "(us_per_call_eager: back-to-back eager launches), inputs in HBM",
            **res}
     if with_cpu:
         out["cpu_baseline"] = cpu_prefill(dev, routers, experts, stride, xs, 64)
