@@ -8,15 +8,15 @@
 //
 // 1. dispatch_kernel: per-expert lists of the (token, slot) pairs, stable in pair order (counts,
 //    row offsets, perm, inverse perm) and the per-expert count of 64-row tiles.
-// 2. grouped_mfma_kernel<2, ...>: for each expert's rows, h = silu(W1 a) * (W3 a) (f32 rows).
-//    grouped_mfma_kernel<1, ...>: y = W2 h (f32 rows). Both on v_mfma_f32_16x16x32_bf16.
+// 2. grouped_gemm_kernel<2>: for each expert's rows, h = silu(W1 a) * (W3 a), written as bf16 hi/lo
+//    planes; grouped_gemm_kernel<1>: y = W2 h (f32 rows). Both on v_mfma_f32_16x16x32_bf16.
 //    The f32 activations are split into bf16 hi + lo parts and both parts are multiplied (two MFMAs
 //    per product). The bf16 weights are exact, so each product keeps ~16 bits of the activation
 //    instead of 8. A full 64-row tile then does 64 rows x 2 parts x 2 flop = 256 flop per weight
 //    element, 128 flop per weight byte: below the bf16 MFMA/HBM ridge (2.5 PFLOP/s / 8 TB/s =
 //    312), so the kernels stay bound by HBM.
-//    Tiles: 64 rows x 64*NB columns per block of 4 waves; K in chunks of KC staged through LDS
-//    (double-buffered); the weight operand streams from HBM into registers one chunk ahead.
+//    Tiles: 64 rows x 256 weight rows per block of 8 waves; the reduction runs in chunks of 64
+//    through a three-stage LDS ring filled by direct HBM -> LDS copies (weights and activations).
 //    Tile order (expert, column tile, row tile), split into 8 contiguous ranges, one per XCD (the
 //    hardware hands block b to XCD b % 8): the row tiles of a hot expert then share each weight
 //    tile in that XCD's L2, and an expert's activation rows are reused across its column tiles.
@@ -44,7 +44,7 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
 // ---------------------------------------------------------------- dispatch (one block, 1024 threads)
 // routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);
 // perm[P]: pair ids grouped by expert, increasing within an expert; pos_of[P]: inverse of perm;
-// m_off[E+1]: exclusive prefix of ceil(counts / 64).
+// m_off[E+1]: exclusive prefix of ceil(counts / kMT).
 // Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
 // equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
 // row; a pair's rank inside its wave's slice goes to pos_of as a temporary. B: wave 0 (4 experts per
@@ -183,7 +183,12 @@ __device__ __forceinline__ void wait_dma() {
 constexpr int kGRows = kMT, kGWRows = 256, kGKC = 64, kGStages = 3;
 constexpr int kGWBytes = kGWRows * 128, kGABytes = kGRows * 128;
 constexpr int kGStageBytes = kGWBytes + 2 * kGABytes;  // 48 KiB
-constexpr int kGDmaPerWave = 6;
+constexpr int kGRG = kGRows / 16;       // row groups of 16 (one per wave)
+constexpr int kGCH = 8 / kGRG;          // weight-row splits (waves per row group)
+constexpr int kGWI = kGWRows / 64;      // weight copies per wave per stage
+constexpr int kGAI = kGRows / 32;       // activation copies per wave per stage
+constexpr int kGDmaPerWave = kGWI + kGAI;
+static_assert(kGStageBytes == 48 * 1024 && kGDmaPerWave == 6 && kGWRows / 16 / kGCH == 8, "tile shape");
 
 __device__ __forceinline__ int swz(int r, int g) { return g ^ ((r >> 1) & 7); }
 
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     constexpr int NTILE = kGWRows / MATS;  // output columns per tile
     __shared__ __align__(1024) uint8_t ring[kGStages * kGStageBytes];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, rg = w & 3, ch = w >> 2;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, rg = w % kGRG, ch = w / kGRG;
     const int ntiles_n = N / NTILE;
     const int total = m_off[E] * ntiles_n;
     const int range = (total + 7) >> 3;
@@ -228,37 +233,48 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
 
     // copy sources of this lane (one pointer per instruction; each stage adds 128 bytes)
-    const uint8_t *wsrc[4];
+    const uint8_t *wsrc[kGWI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = 4 * w + i, r = 8 * t + (lane >> 3), g = swz(r, lane & 7);
+    for (int i = 0; i < kGWI; ++i) {
+        const int t = kGWI * w + i, r = 8 * t + (lane >> 3), g = swz(r, lane & 7);
         const uint8_t *base = experts + (size_t)e * stride + w_off;
         int wr = n0 + r;
         if constexpr (MATS == 2) {
-            if (r >= 128) {
+            if (r >= kGWRows / 2) {
                 base = experts + (size_t)e * stride + w3_off;
-                wr = n0 + r - 128;
+                wr = n0 + r - kGWRows / 2;
             }
         }
         wsrc[i] = base + (size_t)wr * rowb + 16 * g;
     }
-    const uint8_t *asrc[2];
+    const uint8_t *asrc[kGAI];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int u = 2 * w + i, plane = u >> 3, r = 8 * (u & 7) + (lane >> 3), g = swz(r, lane & 7);
+    for (int i = 0; i < kGAI; ++i) {
+        // copy u: plane u / (kGRows / 8), rows 8 * (u % (kGRows / 8)) ..
+        const int u = kGAI * w + i, plane = u / (kGRows / 8), r = 8 * (u % (kGRows / 8)) + (lane >> 3),
+                  g = swz(r, lane & 7);
         const int lr = row0 + (r < rows ? r : 0);  // rows past the list re-read its first row
         const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
         asrc[i] = reinterpret_cast<const uint8_t *>(plane ? a_lo : a_hi) + arow * rowb + 16 * g;
     }
     const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
+    const int nch = Kd / kGKC;
+    // Stage c reads k-chunk (c + rot) mod nch. Without the rotation every resident block streams the
+    // same column window of its rows at the same time, so the whole chip's requests fall on the few
+    // DRAM channels that window maps to. The rotation is a function of the weight tile (expert,
+    // column tile), so the m-tiles that share a tile read it in the same order and stay in step (their
+    // second reads hit L2); the per-output summation order is still fixed for a given input.
+    const int rot = (e * ntiles_n + jt) % nch;
     auto issue = [&](int c) {
         const uint32_t sb = ring0 + (uint32_t)((c % kGStages) * kGStageBytes);
-        const size_t kb = (size_t)c * 128;
+        const int cc = c + rot < nch ? c + rot : c + rot - nch;
+        const size_t kb = (size_t)cc * 128;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (4 * w + i) * 1024));
+        for (int i = 0; i < kGWI; ++i)
+            lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (kGWI * w + i) * 1024));
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + kGWBytes + (2 * w + i) * 1024));
+        for (int i = 0; i < kGAI; ++i)
+            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + kGWBytes + (kGAI * w + i) * 1024));
     };
 
     // MFMA operand reads: lane -> row (lane % 16) of a 16-row block, logical granule 4*ks + lane / 16
@@ -267,7 +283,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     for (int q = 0; q < 8; ++q) {
         int blk;
         if constexpr (MATS == 2)
-            blk = q < 4 ? 4 * ch + q : 8 + 4 * ch + (q - 4);
+            blk = q < 4 ? 4 * ch + q : kGWRows / 32 + 4 * ch + (q - 4);
         else
             blk = 8 * ch + q;
         brow[q] = blk * 16 + (lane & 15);
@@ -279,7 +295,6 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nch = Kd / kGKC;
     issue(0);
     if (nch > 1) issue(1);
     for (int c = 0; c < nch; ++c) {
@@ -445,7 +460,7 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
     e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off);
     if (e != hipSuccess) return e;
     const uint8_t *ex = static_cast<const uint8_t *>(experts);
-    const int max_mtiles = (P + kGRows - 1) / kGRows + E;  // >= sum over experts of ceil(count / 64)
+    const int max_mtiles = (P + kGRows - 1) / kGRows + E;  // >= sum over experts of ceil(count / kGRows)
     // gate/up: N = H, Kd = D, activation rows gathered through perm; h written as hi/lo planes
     e = launch_gemm<2>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, E,
                        max_mtiles, nullptr, h_hi, h_lo);
