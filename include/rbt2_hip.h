@@ -108,6 +108,40 @@ int rbt_hip_matvec(rbt_hip *h, float *out, uint64_t w_offset, const float *x, in
 int rbt_hip_matvec_dev(rbt_hip *h, float *out_dev, const void *W_dev, int dtype, const float *x_dev, int rows,
                        int cols);
 
+/* ---- the whole per-token forward pass (replaces forward(), rabbit2.c:453-548, on the State of
+ * :427-446): embedding, then per layer RMSNorm, q/k/v, QK-norm, RoPE, the KV cache in HBM,
+ * attention, wo + residual and the MoE block, then the final norm and lm_head. The matvecs and
+ * attention sum in parallel orders (results agree with the engine to rounding); the router keeps the
+ * engine's exact order. ---- */
+
+/* Decode state for contexts of up to ctx positions (0 = the engine's default min(max_seq, 512),
+ * larger than max_seq is clamped, rabbit2.c:684-686): the KV cache [n_layers][ctx][kv_dim] f32 (k and
+ * v) and the step buffers, in HBM. Needs an uploaded or created model; replaces any earlier state. */
+int rbt_hip_state_init(rbt_hip *h, int ctx);
+
+/* One forward(token, pos) as the engine's --dump loop calls it (rabbit2.c:703-714): logits [vocab]
+ * and routing_out [n_layers][top_k] (the --dump records, :710-713) in host memory; either may be
+ * NULL. Positions are fed in order 0, 1, ... (the cache holds the positions before pos). Synchronous. */
+int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *routing_out);
+
+/* The engine's --gen loop with greedy sampling (temperature 0, rabbit2.c:716-740): the prompt from
+ * position 0, then up to n_gen tokens (at most ctx - n_prompt; the eos token is kept and ends the
+ * output, -1 = none) into out; *n_out = the count. The loop runs on the device: each step's argmax
+ * writes the next step's token, and each step is one HIP graph replay (steps after an eos are run and
+ * discarded). ms_out (may be NULL) receives [prompt ms, generation ms] from HIP events. */
+int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
+                     int *n_out, double *ms_out);
+
+/* A model image built in place on the device instead of uploaded (no counterpart in the reference,
+ * whose synthetic models are written to files by rabbit2/ref/rbt2.py): validates cfg like
+ * rbt_hip_upload, allocates the image with the file layout (rabbit2.c:158-193) and returns its device
+ * base; the contents are left for the caller to fill. */
+int rbt_hip_model_create(rbt_hip *h, const rbt_config *cfg, void **model_dev);
+/* Byte offset and size of a tensor in the model image (uploaded or created): name is one of
+ * "tok_emb", "final_norm", "lm_head" (layer ignored) or "attn_norm", "wq", "wk", "wv", "wo",
+ * "q_norm", "k_norm", "ffn_norm", "router", "experts" of layer `layer`. */
+int rbt_hip_tensor(rbt_hip *h, const char *name, int layer, uint64_t *offset, uint64_t *bytes);
+
 /* ---- device memory and stream plumbing for hosts without their own HIP code ---- */
 int rbt_hip_malloc(rbt_hip *h, void **dev, uint64_t bytes);
 int rbt_hip_free_dev(rbt_hip *h, void *dev);

@@ -36,6 +36,20 @@ struct Profile {
     uint64_t launches[kProfCount] = {};
 };
 
+// Decode state of the full forward pass (rbt_hip_state_init): one allocation carved into the KV cache
+// and the per-step buffers.
+struct DecodeState {
+    int ctx = 0, S = 0;           // context length, attention splits
+    uint8_t *block = nullptr;     // the allocation
+    float *kc = nullptr, *vc = nullptr;  // [n_layers][ctx][kv_dim]
+    float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr;
+    float *part = nullptr;        // attention split partials [n_heads][S][hd + 2]
+    float *logits = nullptr;      // [vocab]
+    int32_t *routing = nullptr;   // [n_layers][top_k]
+    int32_t *seq = nullptr;       // [ctx] token of each position
+    StepState *st = nullptr;
+};
+
 struct Workspace {
     int tokens = 0, E = 0, K = 0, H = 0;
     float *probs = nullptr;       // [T][E]
@@ -60,6 +74,7 @@ struct rbt_hip {
     uint64_t expert_stride = 0, tok_emb = 0, final_norm = 0, lm_head = 0, layout_end = 0;
     std::vector<LayerOff> layers;
     Workspace ws;
+    DecodeState ds;
     Profile prof;
     int fused_decode = 1;  // option "fused_decode": batch-1 top-k inside the gate/up kernel
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
@@ -233,6 +248,91 @@ int prof_collect(rbt_hip *h) {
     return 1;
 }
 
+// the header checks of load_model (rabbit2.c:199-228)
+bool config_ok(const rbt_config &c) {
+    return !(c.vocab <= 0 || c.dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
+             c.n_experts <= 0 || c.expert_hidden <= 0 || c.max_seq <= 0 || c.top_k <= 0 || c.top_k > c.n_experts ||
+             c.top_k > kMaxTopK || c.head_dim % 2 != 0 || c.n_heads % c.n_kv_heads != 0 ||
+             (c.dtype != RBT_DT_F32 && c.dtype != RBT_DT_BF16));
+}
+
+// (Re)allocates the device image for h->cfg's layout; drops any decode state of an earlier model.
+int model_alloc(rbt_hip *h) {
+    if (!set_device(h)) return 0;
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    (void)hipFree(h->ds.block);
+    h->ds = DecodeState{};
+    if (h->model) {
+        (void)hipFree(h->model);
+        h->model = nullptr;
+        h->model_size = 0;
+    }
+    HIP_OK(h, hipMalloc(&h->model, h->layout_end));
+    h->model_size = h->layout_end;
+    return 1;
+}
+
+// ---- full forward pass: one step = forward(seq[pos], pos) (rabbit2.c:453-548) on the decode state.
+// final: the final norm, lm_head and argmax (which appends the token past the prompt and advances pos);
+// otherwise only pos advances. Everything is enqueued on the handle stream, nothing waits, so a step
+// can be captured into a graph.
+int enqueue_step(rbt_hip *h, bool final) {
+    const rbt_config &c = h->cfg;
+    DecodeState &ds = h->ds;
+    const int D = c.dim, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    const Launch L = lc(h, -1);
+    HIP_OK(h, launch_embed(L, c.dtype, h->model + h->tok_emb, D, c.vocab, ds.st, ds.seq, ds.x));
+    for (int l = 0; l < c.n_layers; l++) {
+        const LayerOff &ly = h->layers[(size_t)l];
+        const void *W[3] = {h->model + ly.wq, h->model + ly.wk, h->model + ly.wv};
+        float *const out[3] = {ds.q, ds.k, ds.v};
+        const int rows[3] = {qd, kvd, kvd};
+        HIP_OK(h, launch_norm_matvec(L, c.dtype, ds.x, reinterpret_cast<const float *>(h->model + ly.attn_norm),
+                                     c.rms_eps, D, W, out, rows));
+        const size_t cache = (size_t)l * ds.ctx * kvd;
+        HIP_OK(h, launch_attention(L, ds.q, ds.k, ds.v,
+                                   c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.q_norm) : ds.q,
+                                   c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.k_norm) : ds.k,
+                                   c.qk_norm, c.rms_eps, c.rope_theta, c.n_heads, c.n_kv_heads, hd, ds.S, ds.ctx,
+                                   ds.st, ds.kc + cache, ds.vc + cache, ds.part));
+        HIP_OK(h, launch_attn_combine(L, ds.part, c.n_heads, hd, ds.S, ds.ao));
+        HIP_OK(h, launch_wo(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
+        HIP_OK(h, launch_rmsnorm(L, ds.x, reinterpret_cast<const float *>(h->model + ly.ffn_norm), D, c.rms_eps,
+                                 ds.xb));
+        rbt_moe_layer ml;
+        if (!rbt_hip_layer(h, l, &ml)) return 0;
+        if (!rbt_hip_moe_dev(h, &ml, ds.xb, 1, ds.x, nullptr, ds.routing + (size_t)l * c.top_k, nullptr)) return 0;
+    }
+    if (final) {
+        const void *W[3] = {h->model + h->lm_head, nullptr, nullptr};
+        float *const out[3] = {ds.logits, nullptr, nullptr};
+        const int rows[3] = {c.vocab, 0, 0};
+        HIP_OK(h, launch_norm_matvec(L, c.dtype, ds.x, reinterpret_cast<const float *>(h->model + h->final_norm),
+                                     c.rms_eps, D, W, out, rows));
+        HIP_OK(h, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx));
+    } else {
+        HIP_OK(h, launch_advance(L, ds.st));
+    }
+    return 1;
+}
+
+// Captures `n` enqueued steps of one kind into an executable graph.
+int capture_step(rbt_hip *h, bool final, hipGraphExec_t *exec) {
+    hipGraph_t g = nullptr;
+    HIP_OK(h, hipStreamBeginCapture(h->stream, hipStreamCaptureModeRelaxed));
+    const int ok = enqueue_step(h, final);
+    const hipError_t e = hipStreamEndCapture(h->stream, &g);
+    if (!ok) {
+        if (g) (void)hipGraphDestroy(g);
+        return 0;
+    }
+    if (e != hipSuccess) return fail(h, "hipStreamEndCapture failed: %s", hipGetErrorString(e));
+    const hipError_t e2 = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e2 != hipSuccess) return fail(h, "hipGraphInstantiate failed: %s", hipGetErrorString(e2));
+    return 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -262,6 +362,7 @@ void rbt_hip_free(rbt_hip *h) {
     (void)hipSetDevice(h->device);
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     ws_release(h->ws);
+    (void)hipFree(h->ds.block);
     for (int k = 0; k < kProfCount; k++)
         for (int j = 0; j < 2; j++)
             if (h->prof.ev[k][j]) (void)hipEventDestroy(h->prof.ev[k][j]);
@@ -289,26 +390,60 @@ int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config 
     if (version != 2) return fail(h, "unsupported .rbt2 version %u (need 2)", version);
     rbt_config c;
     memcpy(&c, d + 8, sizeof c);
-    if (c.vocab <= 0 || c.dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
-        c.n_experts <= 0 || c.expert_hidden <= 0 || c.max_seq <= 0 || c.top_k <= 0 || c.top_k > c.n_experts ||
-        c.top_k > kMaxTopK || c.head_dim % 2 != 0 || c.n_heads % c.n_kv_heads != 0 ||
-        (c.dtype != RBT_DT_F32 && c.dtype != RBT_DT_BF16))
-        return fail(h, "invalid config in header");
+    if (!config_ok(c)) return fail(h, "invalid config in header");
     h->cfg = c;
     compute_layout(h);
     if (h->layout_end > file_size)
         return fail(h, "file too small for its own config (%llu < %llu)", (unsigned long long)file_size,
                     (unsigned long long)h->layout_end);
-    if (!set_device(h)) return 0;
-    if (h->model) {
-        HIP_OK(h, hipStreamSynchronize(h->stream));
-        (void)hipFree(h->model);
-        h->model = nullptr;
-    }
-    HIP_OK(h, hipMalloc(&h->model, h->layout_end));
+    if (!model_alloc(h)) return 0;
     HIP_OK(h, hipMemcpy(h->model, file, h->layout_end, hipMemcpyHostToDevice));
-    h->model_size = h->layout_end;
     if (cfg) *cfg = c;
+    return 1;
+}
+
+int rbt_hip_model_create(rbt_hip *h, const rbt_config *cfg, void **model_dev) {
+    if (!h) return fail(nullptr, "model_create: handle is NULL");
+    if (!cfg || !model_dev) return fail(h, "model_create: NULL argument");
+    *model_dev = nullptr;
+    if (!config_ok(*cfg)) return fail(h, "model_create: invalid config");
+    h->cfg = *cfg;
+    compute_layout(h);
+    if (!model_alloc(h)) return 0;
+    *model_dev = h->model;
+    return 1;
+}
+
+int rbt_hip_tensor(rbt_hip *h, const char *name, int layer, uint64_t *offset, uint64_t *bytes) {
+    if (!h || !name) return fail(h, "tensor: NULL argument");
+    if (!h->model) return fail(h, "tensor: no model");
+    const rbt_config &c = h->cfg;
+    const uint64_t E = c.dtype == RBT_DT_BF16 ? 2 : 4, D = (uint64_t)c.dim;
+    const uint64_t qd = (uint64_t)c.n_heads * c.head_dim, kvd = (uint64_t)c.n_kv_heads * c.head_dim;
+    uint64_t off = 0, n = 0;
+    if (!strcmp(name, "tok_emb")) {
+        off = h->tok_emb, n = (uint64_t)c.vocab * D * E;
+    } else if (!strcmp(name, "final_norm")) {
+        off = h->final_norm, n = D * 4;
+    } else if (!strcmp(name, "lm_head")) {
+        off = h->lm_head, n = (uint64_t)c.vocab * D * E;
+    } else {
+        if (layer < 0 || layer >= c.n_layers) return fail(h, "tensor: layer %d out of range", layer);
+        const LayerOff &ly = h->layers[(size_t)layer];
+        if (!strcmp(name, "attn_norm")) off = ly.attn_norm, n = D * 4;
+        else if (!strcmp(name, "wq")) off = ly.wq, n = qd * D * E;
+        else if (!strcmp(name, "wk")) off = ly.wk, n = kvd * D * E;
+        else if (!strcmp(name, "wv")) off = ly.wv, n = kvd * D * E;
+        else if (!strcmp(name, "wo")) off = ly.wo, n = D * qd * E;
+        else if (!strcmp(name, "q_norm") && c.qk_norm) off = ly.q_norm, n = qd * 4;
+        else if (!strcmp(name, "k_norm") && c.qk_norm) off = ly.k_norm, n = kvd * 4;
+        else if (!strcmp(name, "ffn_norm")) off = ly.ffn_norm, n = D * 4;
+        else if (!strcmp(name, "router")) off = ly.router, n = (uint64_t)c.n_experts * D * E;
+        else if (!strcmp(name, "experts")) off = ly.experts, n = (uint64_t)c.n_experts * h->expert_stride;
+        else return fail(h, "tensor: unknown tensor '%s'", name);
+    }
+    if (offset) *offset = off;
+    if (bytes) *bytes = n;
     return 1;
 }
 
@@ -569,6 +704,149 @@ int rbt_hip_fill_normal(rbt_hip *h, void *dst_dev, int dtype, uint64_t n, uint64
     if (!dst_dev) return fail(h, "fill_normal: NULL pointer");
     if (!set_device(h)) return 0;
     HIP_OK(h, launch_fill_normal(lc(h, -1), dst_dev, dtype, n, seed, stream, first, scale, offset));
+    return 1;
+}
+
+int rbt_hip_state_init(rbt_hip *h, int ctx) {
+    if (!h) return fail(nullptr, "state_init: handle is NULL");
+    if (!h->model) return fail(h, "state_init: no model");
+    const rbt_config &c = h->cfg;
+    if (ctx < 0) return fail(h, "state_init: negative context");
+    if (ctx == 0) ctx = c.max_seq < 512 ? c.max_seq : 512;  // rabbit2.c:684
+    if (ctx > c.max_seq) ctx = c.max_seq;                   // rabbit2.c:685
+    if (!set_device(h)) return 0;
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    (void)hipFree(h->ds.block);
+    h->ds = DecodeState{};
+    DecodeState ds;
+    ds.ctx = ctx;
+    ds.S = ctx / 32 < 1 ? 1 : (ctx / 32 > 16 ? 16 : ctx / 32);  // attention splits over positions
+    const uint64_t D = (uint64_t)c.dim, hd = (uint64_t)c.head_dim, qd = (uint64_t)c.n_heads * hd,
+                   kvd = (uint64_t)c.n_kv_heads * hd;
+    uint64_t off = 0;
+    auto carve = [&](uint64_t bytes) {
+        const uint64_t at = off;
+        off = align_up(off + bytes, 256);
+        return at;
+    };
+    const uint64_t o_kc = carve(4 * (uint64_t)c.n_layers * ctx * kvd), o_vc = carve(4 * (uint64_t)c.n_layers * ctx * kvd);
+    const uint64_t o_x = carve(4 * D), o_xb = carve(4 * D), o_q = carve(4 * qd), o_k = carve(4 * kvd),
+                   o_v = carve(4 * kvd), o_ao = carve(4 * qd);
+    const uint64_t o_part = carve(4 * (uint64_t)c.n_heads * ds.S * (hd + 2));
+    const uint64_t o_lg = carve(4 * (uint64_t)c.vocab), o_rt = carve(4 * (uint64_t)c.n_layers * c.top_k);
+    const uint64_t o_seq = carve(4 * (uint64_t)ctx), o_st = carve(sizeof(StepState));
+    if (attn_lds_bytes(c.head_dim, ctx, ds.S) > 64 * 1024 || 4 * D > 64 * 1024 || 4 * qd > 64 * 1024)
+        return fail(h, "state_init: head_dim/dim/context too large for the attention and matvec kernels");
+    HIP_OK(h, hipMalloc(&ds.block, off));
+    uint8_t *b = ds.block;
+    ds.kc = reinterpret_cast<float *>(b + o_kc);
+    ds.vc = reinterpret_cast<float *>(b + o_vc);
+    ds.x = reinterpret_cast<float *>(b + o_x);
+    ds.xb = reinterpret_cast<float *>(b + o_xb);
+    ds.q = reinterpret_cast<float *>(b + o_q);
+    ds.k = reinterpret_cast<float *>(b + o_k);
+    ds.v = reinterpret_cast<float *>(b + o_v);
+    ds.ao = reinterpret_cast<float *>(b + o_ao);
+    ds.part = reinterpret_cast<float *>(b + o_part);
+    ds.logits = reinterpret_cast<float *>(b + o_lg);
+    ds.routing = reinterpret_cast<int32_t *>(b + o_rt);
+    ds.seq = reinterpret_cast<int32_t *>(b + o_seq);
+    ds.st = reinterpret_cast<StepState *>(b + o_st);
+    HIP_OK(h, hipMemset(ds.block, 0, off));
+    h->ds = ds;
+    // the MoE workspace for one token per layer call, so that no step allocates
+    rbt_moe_layer ml;
+    if (!rbt_hip_layer(h, 0, &ml) || !rbt_hip_reserve(h, &ml, 1)) return 0;
+    return 1;
+}
+
+int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *routing_out) {
+    if (!h) return fail(nullptr, "forward: handle is NULL");
+    if (!h->ds.block) return fail(h, "forward: no decode state (rbt_hip_state_init)");
+    const rbt_config &c = h->cfg;
+    if (token < 0 || token >= c.vocab) return fail(h, "token %d out of range", token);
+    if (pos < 0 || pos >= h->ds.ctx) return fail(h, "forward: position %d outside the context of %d", pos, h->ds.ctx);
+    if (!set_device(h)) return 0;
+    const StepState st{pos, 0x7FFFFFFF, 0, 0};
+    HIP_OK(h, hipMemcpyAsync(h->ds.seq + pos, &token, 4, hipMemcpyHostToDevice, h->stream));
+    HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
+    const bool prof = h->prof.on;
+    h->prof.on = false;  // the step's MoE calls would otherwise wait on their events one by one
+    const int ok = enqueue_step(h, true);
+    h->prof.on = prof;
+    if (!ok) return 0;
+    if (logits) HIP_OK(h, hipMemcpyAsync(logits, h->ds.logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, h->stream));
+    if (routing_out)
+        HIP_OK(h, hipMemcpyAsync(routing_out, h->ds.routing, 4 * (size_t)c.n_layers * c.top_k, hipMemcpyDeviceToHost,
+                                 h->stream));
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    return 1;
+}
+
+int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
+                     int *n_out, double *ms_out) {
+    if (!h) return fail(nullptr, "generate: handle is NULL");
+    if (n_out) *n_out = 0;
+    if (!h->ds.block) return fail(h, "generate: no decode state (rbt_hip_state_init)");
+    const rbt_config &c = h->cfg;
+    const int ctx = h->ds.ctx;
+    if (!prompt || n_prompt < 1) return fail(h, "generate: empty prompt");
+    if (n_prompt > ctx)
+        return fail(h, "prompt has %d tokens but context is %d (use --ctx)", n_prompt, ctx);  // rabbit2.c:687
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= c.vocab) return fail(h, "token %d out of range", prompt[i]);
+    if (n_gen < 0) return fail(h, "generate: negative n_gen");
+    if (n_gen > ctx - n_prompt) n_gen = ctx - n_prompt;  // rabbit2.c:717
+    if (n_gen > 0 && !out) return fail(h, "generate: out is NULL");
+    if (!set_device(h)) return 0;
+    const StepState st{0, n_prompt, 0, 0};
+    HIP_OK(h, hipMemcpyAsync(h->ds.seq, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, h->stream));
+    HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
+    const bool prof = h->prof.on;
+    h->prof.on = false;
+    hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    int ok = capture_step(h, false, &g_adv) && capture_step(h, true, &g_fin);
+    h->prof.on = prof;
+    auto cleanup = [&]() {
+        if (g_adv) (void)hipGraphExecDestroy(g_adv);
+        if (g_fin) (void)hipGraphExecDestroy(g_fin);
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+    };
+    if (!ok) {
+        cleanup();
+        return 0;
+    }
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);
+    if (e == hipSuccess) e = hipEventRecord(ev[0], h->stream);
+    // the prompt: n_prompt forwards, the last one with lm_head + argmax (the first generated token)
+    for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = hipGraphLaunch(g_adv, h->stream);
+    if (e == hipSuccess && n_gen > 0) e = hipGraphLaunch(g_fin, h->stream);
+    if (e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
+    // each further token: one forward of the previous one (rabbit2.c:733)
+    for (int g = 1; g < n_gen && e == hipSuccess; g++) e = hipGraphLaunch(g_fin, h->stream);
+    if (e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+    if (e == hipSuccess && n_gen > 0)
+        e = hipMemcpyAsync(out, h->ds.seq + n_prompt, 4 * (size_t)n_gen, hipMemcpyDeviceToHost, h->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+    if (e == hipSuccess && ms_out) {
+        float a = 0.0f, b = 0.0f;
+        e = hipEventElapsedTime(&a, ev[0], ev[1]);
+        if (e == hipSuccess) e = hipEventElapsedTime(&b, ev[1], ev[2]);
+        ms_out[0] = a;
+        ms_out[1] = b;
+    }
+    cleanup();
+    if (e != hipSuccess) return fail(h, "generate: %s", hipGetErrorString(e));
+    int n = n_gen;
+    for (int g = 0; g < n_gen; g++)
+        if (out[g] == eos) {  // the engine prints the eos token, then stops (rabbit2.c:729-730)
+            n = g + 1;
+            break;
+        }
+    if (n_out) *n_out = n;
     return 1;
 }
 

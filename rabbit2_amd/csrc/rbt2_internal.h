@@ -145,6 +145,29 @@ hipError_t launch_router_prefill(const Launch &L, int dtype, const float *xb, co
                                  int E, int D, int K, int norm_topk, int32_t *routing, float *weights,
                                  uint16_t *x_hi, uint16_t *x_lo);
 
+// ---- full forward pass around the MoE block (model.hip)
+// The step record every forward kernel reads: the position being processed; seq[pos] is its token.
+struct StepState {
+    int32_t pos;       // position of the step being processed
+    int32_t n_prompt;  // prompt length: the argmax appends tokens to seq[] only past it
+    int32_t last;      // the last argmax result
+    int32_t pad;
+};
+hipError_t launch_embed(const Launch &L, int dtype, const void *emb, int D, int vocab, const StepState *st,
+                        const int32_t *seq, float *x);
+// out_s = W_s (x * inv * nw) for up to three row segments (rows[s] may be 0); W_s rows have D elements.
+hipError_t launch_norm_matvec(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
+                              const void *const W[3], float *const out[3], const int rows[3]);
+size_t attn_lds_bytes(int hd, int ctx, int S);
+hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
+                            const float *kw, int qk_norm, float eps, float theta, int n_heads, int n_kv, int hd, int S,
+                            int ctx, const StepState *st, float *kc, float *vc, float *part);
+hipError_t launch_attn_combine(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao);
+hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x);
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out);
+hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx);
+hipError_t launch_advance(const Launch &L, StepState *st);
+
 // Dense matvec (one row per wave).
 hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);
 

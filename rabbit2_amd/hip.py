@@ -20,7 +20,8 @@ EXPORTS = (
     "rbt_hip_layer", "rbt_hip_moe", "rbt_hip_moe_dev", "rbt_hip_reserve", "rbt_hip_expert_counts_dev",
     "rbt_hip_matvec", "rbt_hip_matvec_dev", "rbt_hip_malloc", "rbt_hip_free_dev", "rbt_hip_h2d", "rbt_hip_d2h",
     "rbt_hip_memset_dev", "rbt_hip_synchronize", "rbt_hip_stream", "rbt_hip_fill_normal", "rbt_hip_profile_enable",
-    "rbt_hip_profile_get", "rbt_hip_set_option",
+    "rbt_hip_profile_get", "rbt_hip_set_option", "rbt_hip_state_init", "rbt_hip_forward", "rbt_hip_generate",
+    "rbt_hip_model_create", "rbt_hip_tensor",
 )
 
 
@@ -75,6 +76,11 @@ def lib():
         L.rbt_hip_profile_enable.argtypes = [vp, i32]
         L.rbt_hip_set_option.argtypes = [vp, C.c_char_p, C.c_int64]
         L.rbt_hip_profile_get.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]
+        L.rbt_hip_state_init.argtypes = [vp, i32]
+        L.rbt_hip_forward.argtypes = [vp, i32, i32, vp, vp]
+        L.rbt_hip_generate.argtypes = [vp, vp, i32, i32, C.c_int32, vp, C.POINTER(C.c_int), C.POINTER(C.c_double)]
+        L.rbt_hip_model_create.argtypes = [vp, C.POINTER(Config), C.POINTER(vp)]
+        L.rbt_hip_tensor.argtypes = [vp, C.c_char_p, i32, C.POINTER(u64), C.POINTER(u64)]
         _lib = L
     return _lib
 
@@ -212,6 +218,39 @@ class Device:
         out = np.zeros(rows, np.float32)
         self._check(self.L.rbt_hip_matvec(self.h, _p(out), w_offset, _p(x), rows, x.size))
         return out
+
+    # ---- full forward pass
+    def model_create(self, cfg):
+        """Allocates a model image of cfg's layout on the device; returns its base (c_void_p)."""
+        p = C.c_void_p()
+        self._check(self.L.rbt_hip_model_create(self.h, C.byref(cfg), C.byref(p)))
+        return p
+
+    def tensor(self, name, layer=0):
+        """(byte offset, bytes) of a tensor of the model image."""
+        off, n = C.c_uint64(), C.c_uint64()
+        self._check(self.L.rbt_hip_tensor(self.h, name.encode(), layer, C.byref(off), C.byref(n)))
+        return off.value, n.value
+
+    def state_init(self, ctx=0):
+        self._check(self.L.rbt_hip_state_init(self.h, ctx))
+
+    def forward(self, token, pos, vocab, n_layers, top_k):
+        """forward(token, pos): (logits [vocab], routing [n_layers][top_k])."""
+        logits = np.zeros(vocab, np.float32)
+        routing = np.zeros((n_layers, top_k), np.int32)
+        self._check(self.L.rbt_hip_forward(self.h, int(token), int(pos), _p(logits), _p(routing)))
+        return logits, routing
+
+    def generate(self, prompt, n_gen, eos=-1):
+        """Greedy --gen loop on the device: (generated ids, [prompt ms, generation ms])."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(n_gen, 1), np.int32)
+        n = C.c_int(0)
+        ms = (C.c_double * 2)()
+        self._check(self.L.rbt_hip_generate(self.h, _p(prompt), prompt.size, int(n_gen), int(eos), _p(out),
+                                            C.byref(n), ms))
+        return out[:n.value].tolist(), (ms[0], ms[1])
 
     # ---- device level
     def moe_dev(self, layer, xb, T, x=None, moe=None, routing=None, weights=None):
