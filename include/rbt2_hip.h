@@ -155,9 +155,11 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
  * While enabled, every kernel launch of rbt_hip_moe_dev is bracketed by HIP events on the handle
  * stream and its duration is accumulated under its name ("router", "topk", "gateup",
  * "down_combine"; the grouped path adds "dispatch" -- the activation hi/lo split and the per-expert
- * lists -- and "combine", and its "down_combine" is the down GEMM alone); each call then waits for
- * its own work. rbt_hip_profile_get returns 0 for an unknown
- * name. Meant for measurement passes, not for the timed hot loop. */
+ * lists -- and "combine", and its "down_combine" is the down GEMM alone); rbt_hip_forward adds
+ * "embed", "qkv" (RMSNorm + q/k/v), "attention", "attn_merge", "wo", "ffn_norm", "lm_head" (final
+ * norm + lm_head, with the argmax inside where the rows allow) and "argmax" (otherwise). Each timed launch then waits for its own work (rbt_hip_generate
+ * is never timed this way). rbt_hip_profile_get returns 0 for an unknown name. Meant for
+ * measurement passes, not for the timed hot loop. */
 int rbt_hip_profile_enable(rbt_hip *h, int on);
 int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches);
 

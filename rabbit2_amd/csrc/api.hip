@@ -1,6 +1,7 @@
 // C-ABI of the MoE-layer path (include/rbt2_hip.h): handle, model upload, workspace, dispatch of
 // the gfx950 kernels, and the int 1/0 + stderr error convention of the reference engine
 // (rabbit2/src/rabbit2.c:199-228 for the header checks, :455 for the forward() contract).
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -25,8 +26,14 @@ struct LayerOff {
     uint64_t attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, router, experts;
 };
 
-enum ProfKernel { kProfRouter, kProfTopk, kProfGateup, kProfDown, kProfDispatch, kProfCombine, kProfCount };
-const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_combine", "dispatch", "combine"};
+enum ProfKernel {
+    kProfRouter, kProfTopk, kProfGateup, kProfDown, kProfDispatch, kProfCombine,
+    // the rest of the forward pass (rbt_hip_forward with profiling on)
+    kProfEmbed, kProfQkv, kProfAttn, kProfAttnMerge, kProfWo, kProfFfnNorm, kProfLmHead, kProfArgmax, kProfCount
+};
+const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_combine", "dispatch", "combine",
+                                            "embed", "qkv", "attention", "attn_merge", "wo", "ffn_norm",
+                                            "lm_head", "argmax"};
 
 struct Profile {
     bool on = false;
@@ -44,6 +51,8 @@ struct DecodeState {
     float *kc = nullptr, *vc = nullptr;  // [n_layers][ctx][kv_dim]
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr;
     float *part = nullptr;        // attention split partials [n_heads][S][hd + 2]
+    float2 *rope_cs = nullptr;    // [ctx][hd/2] (cos, sin) of the RoPE angles
+    float2 *cand = nullptr;       // lm_head blocks' argmax candidates
     float *logits = nullptr;      // [vocab]
     int32_t *routing = nullptr;   // [n_layers][top_k]
     int32_t *seq = nullptr;       // [ctx] token of each position
@@ -280,25 +289,41 @@ int enqueue_step(rbt_hip *h, bool final) {
     const rbt_config &c = h->cfg;
     DecodeState &ds = h->ds;
     const int D = c.dim, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
-    const Launch L = lc(h, -1);
-    HIP_OK(h, launch_embed(L, c.dtype, h->model + h->tok_emb, D, c.vocab, ds.st, ds.seq, ds.x));
+    // with profiling on (eager calls only), every launch is timed by its own event pair and collected
+    // right away, since each kernel kind runs once per layer
+#define STEP_LAUNCH(k, call)                  \
+    do {                                      \
+        const Launch L = lc(h, (k));          \
+        HIP_OK(h, (call));                    \
+        if (!prof_collect(h)) return 0;       \
+    } while (0)
+    STEP_LAUNCH(kProfEmbed, launch_embed(L, c.dtype, h->model + h->tok_emb, D, c.vocab, ds.st, ds.seq, ds.x));
     for (int l = 0; l < c.n_layers; l++) {
         const LayerOff &ly = h->layers[(size_t)l];
         const void *W[3] = {h->model + ly.wq, h->model + ly.wk, h->model + ly.wv};
         float *const out[3] = {ds.q, ds.k, ds.v};
         const int rows[3] = {qd, kvd, kvd};
-        HIP_OK(h, launch_norm_matvec(L, c.dtype, ds.x, reinterpret_cast<const float *>(h->model + ly.attn_norm),
-                                     c.rms_eps, D, W, out, rows));
+        const float *attn_norm = reinterpret_cast<const float *>(h->model + ly.attn_norm);
+        if (dense_supported(c.dtype, D, W, rows))
+            STEP_LAUNCH(kProfQkv, launch_dense_norm(L, c.dtype, ds.x, attn_norm, c.rms_eps, D, W, out, rows));
+        else
+            STEP_LAUNCH(kProfQkv, launch_norm_matvec(L, c.dtype, ds.x, attn_norm, c.rms_eps, D, W, out, rows));
         const size_t cache = (size_t)l * ds.ctx * kvd;
-        HIP_OK(h, launch_attention(L, ds.q, ds.k, ds.v,
-                                   c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.q_norm) : ds.q,
-                                   c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.k_norm) : ds.k,
-                                   c.qk_norm, c.rms_eps, c.rope_theta, c.n_heads, c.n_kv_heads, hd, ds.S, ds.ctx,
-                                   ds.st, ds.kc + cache, ds.vc + cache, ds.part));
-        HIP_OK(h, launch_attn_combine(L, ds.part, c.n_heads, hd, ds.S, ds.ao));
-        HIP_OK(h, launch_wo(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
-        HIP_OK(h, launch_rmsnorm(L, ds.x, reinterpret_cast<const float *>(h->model + ly.ffn_norm), D, c.rms_eps,
-                                 ds.xb));
+        STEP_LAUNCH(kProfAttn,
+                    launch_attention(L, ds.q, ds.k, ds.v,
+                                     c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.q_norm) : ds.q,
+                                     c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.k_norm) : ds.k,
+                                     c.qk_norm, c.rms_eps, c.n_heads, c.n_kv_heads, hd, ds.S, ds.st, ds.kc + cache,
+                                     ds.vc + cache, ds.rope_cs, ds.part));
+        const void *Wo[3] = {h->model + ly.wo, nullptr, nullptr};
+        const int wo_rows[3] = {D, 0, 0};
+        STEP_LAUNCH(kProfAttnMerge, launch_attn_merge(L, ds.part, c.n_heads, hd, ds.S, ds.ao));
+        if (dense_supported(c.dtype, qd, Wo, wo_rows))
+            STEP_LAUNCH(kProfWo, launch_dense_resid(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
+        else
+            STEP_LAUNCH(kProfWo, launch_wo(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
+        STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, reinterpret_cast<const float *>(h->model + ly.ffn_norm), D,
+                                                 c.rms_eps, ds.xb));
         rbt_moe_layer ml;
         if (!rbt_hip_layer(h, l, &ml)) return 0;
         if (!rbt_hip_moe_dev(h, &ml, ds.xb, 1, ds.x, nullptr, ds.routing + (size_t)l * c.top_k, nullptr)) return 0;
@@ -307,12 +332,18 @@ int enqueue_step(rbt_hip *h, bool final) {
         const void *W[3] = {h->model + h->lm_head, nullptr, nullptr};
         float *const out[3] = {ds.logits, nullptr, nullptr};
         const int rows[3] = {c.vocab, 0, 0};
-        HIP_OK(h, launch_norm_matvec(L, c.dtype, ds.x, reinterpret_cast<const float *>(h->model + h->final_norm),
-                                     c.rms_eps, D, W, out, rows));
-        HIP_OK(h, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx));
+        const float *fn = reinterpret_cast<const float *>(h->model + h->final_norm);
+        if (dense_supported(c.dtype, D, W, rows)) {  // lm_head and the argmax in one launch
+            STEP_LAUNCH(kProfLmHead, launch_dense_argmax(L, c.dtype, ds.x, fn, c.rms_eps, D, W[0], c.vocab, ds.logits,
+                                                         ds.cand, ds.st, ds.seq, ds.ctx));
+        } else {
+            STEP_LAUNCH(kProfLmHead, launch_norm_matvec(L, c.dtype, ds.x, fn, c.rms_eps, D, W, out, rows));
+            STEP_LAUNCH(kProfArgmax, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx));
+        }
     } else {
-        HIP_OK(h, launch_advance(L, ds.st));
+        STEP_LAUNCH(-1, launch_advance(L, ds.st));
     }
+#undef STEP_LAUNCH
     return 1;
 }
 
@@ -720,7 +751,7 @@ int rbt_hip_state_init(rbt_hip *h, int ctx) {
     h->ds = DecodeState{};
     DecodeState ds;
     ds.ctx = ctx;
-    ds.S = ctx / 32 < 1 ? 1 : (ctx / 32 > 16 ? 16 : ctx / 32);  // attention splits over positions
+    ds.S = ctx / 32 < 1 ? 1 : (ctx / 32 > 16 ? 16 : ctx / 32);  // attention splits over positions (<= 64)
     const uint64_t D = (uint64_t)c.dim, hd = (uint64_t)c.head_dim, qd = (uint64_t)c.n_heads * hd,
                    kvd = (uint64_t)c.n_kv_heads * hd;
     uint64_t off = 0;
@@ -733,10 +764,12 @@ int rbt_hip_state_init(rbt_hip *h, int ctx) {
     const uint64_t o_x = carve(4 * D), o_xb = carve(4 * D), o_q = carve(4 * qd), o_k = carve(4 * kvd),
                    o_v = carve(4 * kvd), o_ao = carve(4 * qd);
     const uint64_t o_part = carve(4 * (uint64_t)c.n_heads * ds.S * (hd + 2));
+    const uint64_t o_rope = carve(8 * (uint64_t)ctx * (hd / 2));
+    const uint64_t o_cand = carve(8 * (uint64_t)dense_argmax_blocks(c.vocab));
     const uint64_t o_lg = carve(4 * (uint64_t)c.vocab), o_rt = carve(4 * (uint64_t)c.n_layers * c.top_k);
     const uint64_t o_seq = carve(4 * (uint64_t)ctx), o_st = carve(sizeof(StepState));
-    if (attn_lds_bytes(c.head_dim, ctx, ds.S) > 64 * 1024 || 4 * D > 64 * 1024 || 4 * qd > 64 * 1024)
-        return fail(h, "state_init: head_dim/dim/context too large for the attention and matvec kernels");
+    if (c.head_dim > 256 || 4 * D > 64 * 1024 || 4 * qd > 64 * 1024)
+        return fail(h, "state_init: head_dim above 256 or dim above 16384 is not supported");
     HIP_OK(h, hipMalloc(&ds.block, off));
     uint8_t *b = ds.block;
     ds.kc = reinterpret_cast<float *>(b + o_kc);
@@ -748,11 +781,30 @@ int rbt_hip_state_init(rbt_hip *h, int ctx) {
     ds.v = reinterpret_cast<float *>(b + o_v);
     ds.ao = reinterpret_cast<float *>(b + o_ao);
     ds.part = reinterpret_cast<float *>(b + o_part);
+    ds.rope_cs = reinterpret_cast<float2 *>(b + o_rope);
+    ds.cand = reinterpret_cast<float2 *>(b + o_cand);
     ds.logits = reinterpret_cast<float *>(b + o_lg);
     ds.routing = reinterpret_cast<int32_t *>(b + o_rt);
     ds.seq = reinterpret_cast<int32_t *>(b + o_seq);
     ds.st = reinterpret_cast<StepState *>(b + o_st);
     HIP_OK(h, hipMemset(ds.block, 0, off));
+    // RoPE (cos, sin) of every position and pair, with the engine's own expressions in double and the
+    // host's libm (rabbit2.c:414-417), so the rotation uses the same floats as the engine
+    {
+        const int half = c.head_dim / 2;
+        std::vector<float2> cs((size_t)ctx * half);
+        for (int p = 0; p < ctx; p++)
+            for (int i = 0; i < half; i++) {
+                const double freq = pow((double)c.rope_theta, -2.0 * i / c.head_dim);
+                const double ang = p * freq;
+                cs[(size_t)p * half + i] = make_float2((float)cos(ang), (float)sin(ang));
+            }
+        const hipError_t e = hipMemcpy(ds.rope_cs, cs.data(), cs.size() * sizeof(float2), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(ds.block);
+            return fail(h, "state_init: hipMemcpy failed: %s", hipGetErrorString(e));
+        }
+    }
     h->ds = ds;
     // the MoE workspace for one token per layer call, so that no step allocates
     rbt_moe_layer ml;
@@ -770,11 +822,7 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
     const StepState st{pos, 0x7FFFFFFF, 0, 0};
     HIP_OK(h, hipMemcpyAsync(h->ds.seq + pos, &token, 4, hipMemcpyHostToDevice, h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
-    const bool prof = h->prof.on;
-    h->prof.on = false;  // the step's MoE calls would otherwise wait on their events one by one
-    const int ok = enqueue_step(h, true);
-    h->prof.on = prof;
-    if (!ok) return 0;
+    if (!enqueue_step(h, true)) return 0;
     if (logits) HIP_OK(h, hipMemcpyAsync(logits, h->ds.logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, h->stream));
     if (routing_out)
         HIP_OK(h, hipMemcpyAsync(routing_out, h->ds.routing, 4 * (size_t)c.n_layers * c.top_k, hipMemcpyDeviceToHost,

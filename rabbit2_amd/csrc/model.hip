@@ -110,39 +110,198 @@ __global__ __launch_bounds__(256) void norm_matvec_kernel(const float *__restric
     if (lane == 0) sg.out[s][r] = v;
 }
 
-// ---------------------------------------------------------------- attention, split over positions
-// grid (n_heads, S). Block (h, s): QK-norm over the whole q and k projections (rabbit2.c:475-478),
-// RoPE of head h's q and of its kv head's k at pos (:479-480), then positions t in its share of
-// [0, pos]: scores q.k_t / sqrt(hd) (:486-492), local max m, l = sum exp(score - m), o = sum exp(score -
-// m) v_t. The current position's k and v are used from registers; block (h, 0) of the first query head
-// of each kv head appends them to the cache (:482-484). part[(h*S + s)*(hd + 2)]: m, l, o[hd].
-__device__ __forceinline__ void rope_pair(float *p, int i, int half, int hd, int pos, float theta) {
-#pragma clang fp contract(off)
-    const double freq = pow((double)theta, -2.0 * i / hd);
-    const double ang = pos * freq;
-    const float cs = (float)cos(ang), sn = (float)sin(ang);
-    const float a = p[i], b = p[i + half];
-    p[i] = a * cs - b * sn;
-    p[i + half] = b * cs + a * sn;
+// ---------------------------------------------------------------- dense matvec, many rows per wave
+// Rows of D = NC * 64 * kPer elements (D a multiple of 512 bf16 / 256 f32): each wave takes RPW
+// consecutive rows and issues all RPW * NC of its 16-byte loads before the input vector is staged,
+// so the weight stream is in flight while the block computes the RMSNorm (MODE 0/2) or stages the
+// attention output (MODE 1).
+//   MODE 0: out_s[r] = W_s[r] . (x * inv * nw)          (q/k/v: up to three row segments)
+//   MODE 1: x[r] += W[r] . a (wo + residual, rabbit2.c:500-501)
+//   MODE 2: out[r] = W[r] . (x * inv * nw), and the block's argmax candidate (largest value, first
+//           index) to cand[block] for argmax_cand_kernel (lm_head, rabbit2.c:545-546)
+template <int DT, int NC, int RPW, int MODE>
+__global__ __launch_bounds__(256) void dense_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                    float eps, Segs sg, int total_rows, float *__restrict__ resid,
+                                                    float2 *__restrict__ cand) {
+    constexpr int kPer = DT == RBT_DT_BF16 ? 8 : 4, kEsz = DT == RBT_DT_BF16 ? 2 : 4;
+    constexpr int D = NC * kWave * kPer;
+    __shared__ __align__(16) float xs[D];
+    __shared__ float red[16];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r0 = (blockIdx.x * 4 + wv) * RPW;
+    // weights first: row r0 + j (clamped into range; clamped rows are computed and dropped)
+    u32x4 w[RPW][NC];
+    int seg[RPW], row[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        int r = min(r0 + j, total_rows - 1), s = 0;
+        while (s < 2 && r >= sg.rows[s]) {
+            r -= sg.rows[s];
+            ++s;
+        }
+        seg[j] = s;
+        row[j] = r;
+        const uint8_t *src = sg.W[s] + (size_t)r * D * kEsz;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) w[j][i] = ld_stream_u4(src + (size_t)(lane + kWave * i) * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MODE == 1) {
+        for (int i = threadIdx.x; i < D; i += blockDim.x) xs[i] = x[i];
+    } else {
+        const float inv = rms_inv(x, D, eps, red);
+        for (int i = threadIdx.x; i < D; i += blockDim.x) xs[i] = x[i] * inv * nw[i];
+    }
+    __syncthreads();
+    float acc[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        acc[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const float *xp = xs + (lane + kWave * i) * kPer;
+            if constexpr (DT == RBT_DT_BF16) {
+                const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xp), x1 = *reinterpret_cast<const f32x4 *>(xp + 4);
+                const u32x4 v = w[j][i];
+                acc[j] += bf16_lo(v.x) * x0.x + bf16_hi(v.x) * x0.y + bf16_lo(v.y) * x0.z + bf16_hi(v.y) * x0.w +
+                          bf16_lo(v.z) * x1.x + bf16_hi(v.z) * x1.y + bf16_lo(v.w) * x1.z + bf16_hi(v.w) * x1.w;
+            } else {
+                const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xp);
+                const u32x4 v = w[j][i];
+                acc[j] += __uint_as_float(v.x) * x0.x + __uint_as_float(v.y) * x0.y + __uint_as_float(v.z) * x0.z +
+                          __uint_as_float(v.w) * x0.w;
+            }
+        }
+    }
+    float best = -INFINITY;
+    int bi = -1;
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        const float v = wave_sum(acc[j]);
+        const bool valid = r0 + j < total_rows;
+        if (lane == 0 && valid) {
+            if constexpr (MODE == 1)
+                resid[row[j]] = resid[row[j]] + v;
+            else
+                sg.out[seg[j]][row[j]] = v;
+        }
+        if constexpr (MODE == 2) {
+            if (valid && v == v && (bi < 0 || v > best)) {  // rows ascend: equal values keep the first
+                best = v;
+                bi = r0 + j;
+            }
+        }
+    }
+    if constexpr (MODE == 2) {
+        __shared__ float s_b[4];
+        __shared__ int s_i[4];
+        if (lane == 0) {
+            s_b[wv] = best;
+            s_i[wv] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float b = -INFINITY;
+            int k = -1;
+            for (int q = 0; q < 4; ++q)
+                if (s_i[q] >= 0 && (k < 0 || s_b[q] > b || (s_b[q] == b && s_i[q] < k))) {
+                    b = s_b[q];
+                    k = s_i[q];
+                }
+            cand[blockIdx.x] = make_float2(b, __int_as_float(k));
+        }
+    }
 }
+
+// Greedy argmax over the lm_head blocks' candidates (value, first index; index -1 = none), then the step
+// advances like argmax_kernel: the engine's scan keeps index 0 when logits[0] is NaN or nothing beats it.
+__global__ __launch_bounds__(1024) void argmax_cand_kernel(const float2 *__restrict__ cand, int nc,
+                                                           const float *__restrict__ logits, StepState *st,
+                                                           int32_t *__restrict__ seq, int ctx) {
+    __shared__ float s_b[16];
+    __shared__ int s_i[16];
+    float b = -INFINITY;
+    int k = -1;
+    for (int q = threadIdx.x; q < nc; q += blockDim.x) {
+        const float2 c = cand[q];
+        const int ci = __float_as_int(c.y);
+        if (ci >= 0 && (k < 0 || c.x > b || (c.x == b && ci < k))) {
+            b = c.x;
+            k = ci;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_down(b, off, 64);
+        const int ok = __shfl_down(k, off, 64);
+        if (ok >= 0 && (k < 0 || ob > b || (ob == b && ok < k))) {
+            b = ob;
+            k = ok;
+        }
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    if (lane == 0) {
+        s_b[wv] = b;
+        s_i[wv] = k;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        b = -INFINITY;
+        k = -1;
+        for (int q = 0; q < (int)(blockDim.x >> 6); ++q)
+            if (s_i[q] >= 0 && (k < 0 || s_b[q] > b || (s_b[q] == b && s_i[q] < k))) {
+                b = s_b[q];
+                k = s_i[q];
+            }
+        const float v0 = logits[0];
+        if (k < 0 || v0 != v0) k = 0;
+        const int p = st->pos;
+        st->last = k;
+        if (p + 1 < ctx && p + 1 >= st->n_prompt) seq[p + 1] = k;
+        st->pos = p + 1;
+    }
+}
+
+// ---------------------------------------------------------------- attention, split over positions
+// grid (n_heads, S). Block (h, s): QK-norm over the whole q and k projections (rabbit2.c:475-478), RoPE
+// of head h's q and of its kv head's k at pos (:479-480) from the [ctx][hd/2] (cos, sin) table, then the
+// positions t of its share of [0, pos]: scores q.k_t / sqrt(hd) (:486-492), and per wave an online
+// softmax (running max m, l = sum exp(score - m), o = sum exp(score - m) v_t) over its positions, the
+// K and V rows of KG positions in flight at once. The four waves merge into the block's partial
+// (m, l, o), which the wo kernel merges across the S splits (:493-498). The current position's k and v
+// come from registers; block (h, 0) of the first query head of each kv head appends them to the cache
+// (:482-484).
+constexpr int kAttnMaxE = 4;  // head_dim <= 256: at most 4 elements per lane
+constexpr int kAttnKG = 8;    // positions per wave per round
 
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_raw, const float *__restrict__ k_raw,
                                                    const float *__restrict__ v_raw, const float *__restrict__ qw,
-                                                   const float *__restrict__ kw, int qk_norm, float eps, float theta,
-                                                   int n_heads, int n_kv, int hd, int S, int ctx,
-                                                   const StepState *__restrict__ st, float *__restrict__ kc,
-                                                   float *__restrict__ vc, float *__restrict__ part) {
-    extern __shared__ __align__(16) float sm[];  // q[hd], k[hd], v[hd], scores[chunk]
-    __shared__ float red[16];
-    float *qh = sm, *kh = sm + hd, *vh = sm + 2 * hd, *sc = sm + 3 * hd;
-    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+                                                   const float *__restrict__ kw, int qk_norm, float eps, int n_heads,
+                                                   int n_kv, int hd, int S, const StepState *__restrict__ st,
+                                                   float *__restrict__ kc, float *__restrict__ vc,
+                                                   const float2 *__restrict__ rope_cs, float *__restrict__ part) {
+    __shared__ __align__(16) float qh[256], kh[256], vh[256];
+    __shared__ float red[16], w_m[4], w_l[4];
+    __shared__ __align__(16) float w_o[4][256];
+    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int group = n_heads / n_kv, kvh = h / group;
     const int q_dim = n_heads * hd, kv_dim = n_kv * hd, half = hd / 2;
     const int pos = st->pos;
     float inv_q = 1.0f, inv_k = 1.0f;
-    if (qk_norm) {
-        inv_q = rms_inv(q_raw, q_dim, eps, red);
-        inv_k = rms_inv(k_raw, kv_dim, eps, red);
+    if (qk_norm) {  // both sums of squares in one pass, one reduction
+        float sq = 0.0f, sk = 0.0f;
+        for (int i = tid; i < q_dim; i += blockDim.x) sq += q_raw[i] * q_raw[i];
+        for (int i = tid; i < kv_dim; i += blockDim.x) sk += k_raw[i] * k_raw[i];
+        sq = wave_sum(sq);
+        sk = wave_sum(sk);
+        if (lane == 0) {
+            red[wv] = sq;
+            red[8 + wv] = sk;
+        }
+        __syncthreads();
+        sq = (red[0] + red[1]) + (red[2] + red[3]);
+        sk = (red[8] + red[9]) + (red[10] + red[11]);
+        inv_q = 1.0f / sqrtf(sq / (float)q_dim + eps);
+        inv_k = 1.0f / sqrtf(sk / (float)kv_dim + eps);
     }
     for (int i = tid; i < hd; i += blockDim.x) {
         const int qi = h * hd + i, ki = kvh * hd + i;
@@ -152,8 +311,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
     }
     __syncthreads();
     for (int i = tid; i < half; i += blockDim.x) {
-        rope_pair(qh, i, half, hd, pos, theta);
-        rope_pair(kh, i, half, hd, pos, theta);
+#pragma clang fp contract(off)
+        const float2 cs = rope_cs[(size_t)pos * half + i];
+        float a = qh[i], b = qh[i + half];
+        qh[i] = a * cs.x - b * cs.y;
+        qh[i + half] = b * cs.x + a * cs.y;
+        a = kh[i];
+        b = kh[i + half];
+        kh[i] = a * cs.x - b * cs.y;
+        kh[i + half] = b * cs.x + a * cs.y;
     }
     __syncthreads();
     if (s == 0 && h % group == 0) {
@@ -165,77 +331,104 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
     }
     const int n = pos + 1;
     const int chunk = (n + S - 1) / S;
-    const int t0 = s * chunk, t1 = min(n, t0 + chunk);
-    float *po = part + ((size_t)h * S + s) * (hd + 2);
-    if (t0 >= t1) {  // block-uniform: this split has no positions
-        if (tid == 0) {
-            po[0] = -INFINITY;
-            po[1] = 0.0f;
-        }
-        for (int i = tid; i < hd; i += blockDim.x) po[2 + i] = 0.0f;
-        return;
-    }
+    const int t0 = min(n, s * chunk), t1 = min(n, t0 + chunk);
     const float scale = 1.0f / sqrtf((float)hd);
-    const int lane = tid & 63, wv = tid >> 6, nwv = blockDim.x >> 6;
-    for (int t = t0 + wv; t < t1; t += nwv) {
-        const float *kt = t == pos ? kh : kc + (size_t)t * kv_dim + (size_t)kvh * hd;
-        float d = 0.0f;
-        for (int i = lane; i < hd; i += kWave) d += qh[i] * kt[i];
-        d = wave_sum(d);
-        if (lane == 0) sc[t - t0] = d * scale;
+    float q[kAttnMaxE], o[kAttnMaxE];
+#pragma unroll
+    for (int e = 0; e < kAttnMaxE; ++e) {
+        const int i = lane + kWave * e;
+        q[e] = i < hd ? qh[i] : 0.0f;
+        o[e] = 0.0f;
     }
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int t = tid; t < t1 - t0; t += blockDim.x) mx = fmaxf(mx, sc[t]);
-    mx = wave_max(mx);
-    __syncthreads();
-    if (lane == 0) red[wv] = mx;
-    __syncthreads();
-    mx = red[0];
-    for (int i = 1; i < nwv; ++i) mx = fmaxf(mx, red[i]);
-    float l = 0.0f;
-    for (int t = tid; t < t1 - t0; t += blockDim.x) {
-        const float e = expf(sc[t] - mx);
-        sc[t] = e;
-        l += e;
-    }
-    l = block_sum(l, red);  // its leading barrier also publishes sc[]
-    for (int i = tid; i < hd; i += blockDim.x) {
-        float o = 0.0f;
-        for (int t = t0; t < t1; ++t) {
-            const float vt = t == pos ? vh[i] : vc[(size_t)t * kv_dim + (size_t)kvh * hd + i];
-            o += sc[t - t0] * vt;
+    float m = -INFINITY, l = 0.0f;
+    for (int tb = t0 + wv * kAttnKG; tb < t1; tb += 4 * kAttnKG) {  // wave-uniform rounds
+        float kr[kAttnKG][kAttnMaxE], vr[kAttnKG][kAttnMaxE];
+#pragma unroll
+        for (int g = 0; g < kAttnKG; ++g) {
+            const int t = min(tb + g, t1 - 1);  // past the share: a repeat of the last row, weight 0 below
+            const float *kt = t == pos ? kh : kc + (size_t)t * kv_dim + (size_t)kvh * hd;
+            const float *vt = t == pos ? vh : vc + (size_t)t * kv_dim + (size_t)kvh * hd;
+#pragma unroll
+            for (int e = 0; e < kAttnMaxE; ++e) {
+                const int i = lane + kWave * e;
+                kr[g][e] = i < hd ? kt[i] : 0.0f;
+                vr[g][e] = i < hd ? vt[i] : 0.0f;
+            }
         }
-        po[2 + i] = o;
+        float sc[kAttnKG];
+#pragma unroll
+        for (int g = 0; g < kAttnKG; ++g) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < kAttnMaxE; ++e) d += q[e] * kr[g][e];
+            sc[g] = tb + g < t1 ? wave_sum(d) * scale : -INFINITY;
+        }
+        float mn = m;
+#pragma unroll
+        for (int g = 0; g < kAttnKG; ++g) mn = fmaxf(mn, sc[g]);
+        const float alpha = expf(m - mn);  // m = -inf on the first round: alpha 0
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < kAttnMaxE; ++e) o[e] *= alpha;
+#pragma unroll
+        for (int g = 0; g < kAttnKG; ++g) {
+            const float p = expf(sc[g] - mn);  // positions past the share: exp(-inf) = 0
+            l += p;
+#pragma unroll
+            for (int e = 0; e < kAttnMaxE; ++e) o[e] += p * vr[g][e];
+        }
+        m = mn;
     }
+    // merge the four waves
+    if (lane == 0) {
+        w_m[wv] = m;
+        w_l[wv] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < kAttnMaxE; ++e) {
+        const int i = lane + kWave * e;
+        if (i < hd) w_o[wv][i] = o[e];
+    }
+    __syncthreads();
+    float *po = part + ((size_t)h * S + s) * (hd + 2);
+    const float M = fmaxf(fmaxf(w_m[0], w_m[1]), fmaxf(w_m[2], w_m[3]));
+    float sw[4];
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        sw[w] = w_l[w] > 0.0f ? expf(w_m[w] - M) : 0.0f;
+        L += sw[w] * w_l[w];
+    }
+    for (int i = tid; i < hd; i += blockDim.x)
+        po[2 + i] = ((sw[0] * w_o[0][i] + sw[1] * w_o[1][i]) + (sw[2] * w_o[2][i] + sw[3] * w_o[3][i]));
     if (tid == 0) {
-        po[0] = mx;
-        po[1] = l;
+        po[0] = M;
+        po[1] = L;
     }
 }
 
-// ---------------------------------------------------------------- attention combine
-// Block h merges the S split partials of head h: M = max m_s, L = sum exp(m_s - M) l_s,
-// attn_out[h*hd + i] = sum exp(m_s - M) o_s[i] / L (the engine's softmax-weighted sum, :493-498).
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float *__restrict__ part, int hd, int S,
-                                                           float *__restrict__ ao) {
+// attn_out[h*hd + i] = sum_s a_s o_s[i] / sum_s a_s l_s with a_s = exp(m_s - max m): block h merges the
+// S split partials of head h (the engine's softmax-weighted sum over all positions, rabbit2.c:493-498).
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part, int hd, int S,
+                                                         float *__restrict__ ao) {
+    __shared__ float wa[64], s_inv;
     const int h = blockIdx.x;
     const float *ph = part + (size_t)h * S * (hd + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, ph[(size_t)s * (hd + 2)]);
-    float L = 0.0f;
-    for (int s = 0; s < S; ++s) {
-        const float *p = ph + (size_t)s * (hd + 2);
-        if (p[1] > 0.0f) L += expf(p[0] - M) * p[1];
+    if (threadIdx.x < 64) {  // S <= 64 split weights, by wave 0
+        const int q = threadIdx.x;
+        const float m = q < S ? ph[(size_t)q * (hd + 2)] : -INFINITY;
+        const float l = q < S ? ph[(size_t)q * (hd + 2) + 1] : 0.0f;
+        const float M = wave_max(m);
+        const float a = l > 0.0f ? expf(m - M) : 0.0f;
+        wa[q] = a;
+        const float L = wave_sum(a * l);
+        if (q == 0) s_inv = 1.0f / L;
     }
-    const float invL = 1.0f / L;
+    __syncthreads();
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
         float o = 0.0f;
-        for (int s = 0; s < S; ++s) {
-            const float *p = ph + (size_t)s * (hd + 2);
-            if (p[1] > 0.0f) o += expf(p[0] - M) * p[2 + i];
-        }
-        ao[(size_t)h * hd + i] = o * invL;
+        for (int q = 0; q < S; ++q) o += wa[q] * ph[(size_t)q * (hd + 2) + 2 + i];
+        ao[(size_t)h * hd + i] = o * s_inv;
     }
 }
 
@@ -320,6 +513,46 @@ __global__ void advance_kernel(StepState *st) {
 
 inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The specialised dense kernel when rows are whole 1 KiB wave-steps (D = 512 * NC bf16 / 256 * NC f32,
+// NC in 1..8), else nullopt-like false. mode: 0 norm + matvec, 1 matvec + residual, 2 lm_head + argmax.
+bool dense_ok(int dtype, int D, const void *const W[3], const int rows[3]) {
+    const int step = dtype == RBT_DT_BF16 ? 512 : 256;
+    if (D % step != 0 || D / step < 1 || D / step > 8) return false;
+    for (int i = 0; i < 3; ++i)
+        if (rows[i] > 0 && !al16(W[i])) return false;
+    return true;
+}
+
+template <int DT, int MODE>
+hipError_t dense_dt(const Launch &L, int D, const float *x, const float *nw, float eps, const Segs &sg, int total,
+                    float *resid, float2 *cand) {
+    constexpr int step = DT == RBT_DT_BF16 ? 512 : 256;
+    constexpr int RPW = 4;
+    const dim3 g((unsigned)((total + 4 * RPW - 1) / (4 * RPW))), b(256);
+    switch (D / step) {
+#define DENSE_CASE(nc) \
+    case nc:           \
+        return launch(L, dense_kernel<DT, nc, RPW, MODE>, g, b, 0, x, nw, eps, sg, total, resid, cand);
+        DENSE_CASE(1)
+        DENSE_CASE(2)
+        DENSE_CASE(3)
+        DENSE_CASE(4)
+        DENSE_CASE(5)
+        DENSE_CASE(6)
+        DENSE_CASE(7)
+        DENSE_CASE(8)
+#undef DENSE_CASE
+        default:
+            return hipErrorNotSupported;
+    }
+}
+
+template <int MODE>
+hipError_t launch_dense_mode(const Launch &L, int dtype, int D, const float *x, const float *nw, float eps,
+                             const Segs &sg, int total, float *resid, float2 *cand) {
+    return dtype == RBT_DT_BF16 ? dense_dt<RBT_DT_BF16, MODE>(L, D, x, nw, eps, sg, total, resid, cand)
+                                : dense_dt<RBT_DT_F32, MODE>(L, D, x, nw, eps, sg, total, resid, cand);
+}
 }  // namespace
 
 hipError_t launch_embed(const Launch &L, int dtype, const void *emb, int D, int vocab, const StepState *st,
@@ -352,17 +585,59 @@ hipError_t launch_norm_matvec(const Launch &L, int dtype, const float *x, const 
                : launch(L, norm_matvec_kernel<RBT_DT_F32, false>, g, b, lds, x, nw, eps, D, sg, total);
 }
 
-size_t attn_lds_bytes(int hd, int ctx, int S) { return 4 * (3 * (size_t)hd + (size_t)((ctx + S - 1) / S)); }
-
-hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
-                            const float *kw, int qk_norm, float eps, float theta, int n_heads, int n_kv, int hd, int S,
-                            int ctx, const StepState *st, float *kc, float *vc, float *part) {
-    return launch(L, attn_kernel, dim3((unsigned)n_heads, (unsigned)S), dim3(256), (uint32_t)attn_lds_bytes(hd, ctx, S),
-                  q, k, v, qw, kw, qk_norm, eps, theta, n_heads, n_kv, hd, S, ctx, st, kc, vc, part);
+bool dense_supported(int dtype, int D, const void *const W[3], const int rows[3]) {
+    return dense_ok(dtype, D, W, rows);
 }
 
-hipError_t launch_attn_combine(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao) {
-    return launch(L, attn_combine_kernel, dim3((unsigned)n_heads), dim3(256), 0, part, hd, S, ao);
+hipError_t launch_dense_norm(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
+                             const void *const W[3], float *const out[3], const int rows[3]) {
+    Segs sg;
+    int total = 0;
+    for (int i = 0; i < 3; ++i) {
+        sg.W[i] = static_cast<const uint8_t *>(W[i]);
+        sg.out[i] = out[i];
+        sg.rows[i] = rows[i];
+        total += rows[i];
+    }
+    if (total == 0) return hipSuccess;
+    return launch_dense_mode<0>(L, dtype, D, x, nw, eps, sg, total, nullptr, nullptr);
+}
+
+hipError_t launch_dense_resid(const Launch &L, int dtype, const float *a, int cols, const void *W, int rows,
+                              float *x) {
+    Segs sg{};
+    sg.W[0] = static_cast<const uint8_t *>(W);
+    sg.rows[0] = rows;
+    return launch_dense_mode<1>(L, dtype, cols, a, nullptr, 0.0f, sg, rows, x, nullptr);
+}
+
+int dense_argmax_blocks(int rows) { return (rows + 15) / 16; }
+
+hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
+                               const void *W, int rows, float *logits, float2 *cand, StepState *st, int32_t *seq,
+                               int ctx) {
+    Segs sg{};
+    sg.W[0] = static_cast<const uint8_t *>(W);
+    sg.out[0] = logits;
+    sg.rows[0] = rows;
+    hipError_t e = launch_dense_mode<2>(L, dtype, D, x, nw, eps, sg, rows, nullptr, cand);
+    if (e != hipSuccess) return e;
+    Launch L2 = L;  // the event pair (if any) brackets the first launch only
+    L2.start = L2.stop = nullptr;
+    return launch(L2, argmax_cand_kernel, dim3(1), dim3(1024), 0, (const float2 *)cand, dense_argmax_blocks(rows),
+                  (const float *)logits, st, seq, ctx);
+}
+
+hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
+                            const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
+                            const StepState *st, float *kc, float *vc, const float2 *rope_cs, float *part) {
+    if (hd > kWave * kAttnMaxE) return hipErrorInvalidValue;
+    return launch(L, attn_kernel, dim3((unsigned)n_heads, (unsigned)S), dim3(256), 0, q, k, v, qw, kw, qk_norm, eps,
+                  n_heads, n_kv, hd, S, st, kc, vc, rope_cs, part);
+}
+
+hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao) {
+    return launch(L, attn_merge_kernel, dim3((unsigned)n_heads), dim3(256), 0, part, hd, S, ao);
 }
 
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x) {

@@ -158,11 +158,26 @@ hipError_t launch_embed(const Launch &L, int dtype, const void *emb, int D, int 
 // out_s = W_s (x * inv * nw) for up to three row segments (rows[s] may be 0); W_s rows have D elements.
 hipError_t launch_norm_matvec(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
                               const void *const W[3], float *const out[3], const int rows[3]);
-size_t attn_lds_bytes(int hd, int ctx, int S);
+// The same with many rows per wave and every weight load issued first, for rows of whole 1 KiB
+// wave-steps (D a multiple of 512 bf16 / 256 f32, at most 8 steps) -- dense_supported(). _resid: x[r] +=
+// W[r] . a (wo). _argmax: the
+// final norm + lm_head rows with one (value, index) candidate per block (dense_argmax_blocks(rows) of
+// them), then a one-block launch that reduces them, advances the step and appends the token.
+bool dense_supported(int dtype, int D, const void *const W[3], const int rows[3]);
+hipError_t launch_dense_norm(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
+                             const void *const W[3], float *const out[3], const int rows[3]);
+hipError_t launch_dense_resid(const Launch &L, int dtype, const float *a, int cols, const void *W, int rows, float *x);
+int dense_argmax_blocks(int rows);
+hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
+                               const void *W, int rows, float *logits, float2 *cand, StepState *st, int32_t *seq,
+                               int ctx);
+// Attention of one step: grid (n_heads, S splits of the positions), each block writes its partial
+// (m, l, o[hd]) to part [n_heads][S][hd + 2]; launch_attn_merge merges them into ao (S <= 64).
+// rope_cs: [ctx][hd/2] (cos, sin) of the engine's RoPE angles. hd <= 256.
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
-                            const float *kw, int qk_norm, float eps, float theta, int n_heads, int n_kv, int hd, int S,
-                            int ctx, const StepState *st, float *kc, float *vc, float *part);
-hipError_t launch_attn_combine(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao);
+                            const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
+                            const StepState *st, float *kc, float *vc, const float2 *rope_cs, float *part);
+hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao);
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x);
 hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out);
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx);

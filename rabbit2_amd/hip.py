@@ -224,6 +224,7 @@ class Device:
         """Allocates a model image of cfg's layout on the device; returns its base (c_void_p)."""
         p = C.c_void_p()
         self._check(self.L.rbt_hip_model_create(self.h, C.byref(cfg), C.byref(p)))
+        self.model_base = p
         return p
 
     def tensor(self, name, layer=0):
