@@ -14,8 +14,10 @@ the model is not part of this path).
 Prints one JSON line: tok/s of the 16-layer MoE stack; the roofline of the dominant kernel
 (expert gate/up GEMV) from HIP events on the stream it runs on; the whole-layer HBM rate; the
 512-token prefill of layer 0 ("prefill": uniform and skewed routing, tokens-per-expert histogram,
-HBM rate and matrix-core utilisation of the grouped GEMMs); and the CPU baseline (the oracle's
-AVX2-order path on one host core, the engine's own arithmetic).
+HBM rate and matrix-core utilisation of the grouped GEMMs); the whole OLMoE-1B-7B-shaped model
+("full_model": 16 layers with attention, vocab 50304, a 128-token prompt and 256 greedy tokens
+through the device-side generate loop); and the CPU baselines (the oracle, the engine's own
+arithmetic in its AVX2 order, on one host core).
 """
 import argparse
 import ctypes as C
@@ -92,6 +94,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target length of the CPU baseline sample")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill leg")
     ap.add_argument("--prefill-reps", type=int, default=20, help="timed calls per prefill workload")
+    ap.add_argument("--no-full-model", action="store_true", help="skip the whole-model generate leg")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one device-to-device copy of this size (a known-size kernel for scaling "
                          "FETCH_SIZE/WRITE_SIZE counters)")
@@ -292,8 +295,116 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(dev, routers, experts, stride, xs_host, args.cpu_seconds)
 
+    if not args.no_full_model:
+        out["full_model"] = full_model_leg(not args.no_cpu, args.cpu_seconds)
+
     print(json.dumps(out), flush=True)
     dev.close()
+
+
+# The whole model at the OLMoE-1B-7B shape (16 layers, 16 heads x 128 with QK-norm and RoPE, 64
+# experts top-8, SwiGLU 1024, vocab 50304, bf16 weights ~N(0, 0.02), norm weights 1.0, OLMoE's
+# un-renormalised top-8).
+FULL_CFG = dict(vocab=50304, dim=2048, n_layers=16, n_heads=16, n_kv_heads=16, head_dim=128, n_experts=64, top_k=8,
+                expert_hidden=1024, max_seq=4096, dtype=1, qk_norm=1, norm_topk=0, rope_theta=10000.0, rms_eps=1e-5)
+N_PROMPT, N_GEN = 128, 256
+FULL_MATS = ("wq", "wk", "wv", "wo", "router", "experts")
+FULL_NORMS = ("attn_norm", "q_norm", "k_norm", "ffn_norm")
+
+
+def full_model_leg(with_cpu, cpu_seconds):
+    """128 random prompt ids, then 256 greedy tokens through rbt_hip_generate (one HIP graph replay
+    per token, the argmax feeding the next step on the device). Reports generated tok/s, prompt tok/s
+    and the weight bytes streamed per generated token."""
+    from rabbit2_amd import hip as rh
+    dev = rh.Device(0)
+    cfg = rh.Config(**FULL_CFG)
+    t0 = time.time()
+    base = dev.model_create(cfg)
+    fill = dev.L.rbt_hip_fill_normal
+    sid = [0x4D00]
+
+    def fill_tensor(name, layer, dtype, scale, offset):
+        off, nbytes = dev.tensor(name, layer)
+        sid[0] += 1
+        dev._check(fill(dev.h, C.c_void_p(base.value + off), dtype, nbytes // (2 if dtype == rh.DT_BF16 else 4),
+                        SEED, sid[0], 0, scale, offset))
+
+    fill_tensor("tok_emb", 0, rh.DT_BF16, W_SCALE, 0.0)
+    for l in range(cfg.n_layers):
+        for name in FULL_MATS:
+            fill_tensor(name, l, rh.DT_BF16, W_SCALE, 0.0)  # the expert blobs' alignment padding is filled too
+        for name in FULL_NORMS:
+            fill_tensor(name, l, rh.DT_F32, 0.0, 1.0)
+    fill_tensor("final_norm", 0, rh.DT_F32, 0.0, 1.0)
+    fill_tensor("lm_head", 0, rh.DT_BF16, W_SCALE, 0.0)
+    dev.synchronize()
+    setup_s = time.time() - t0
+    dev.set_router_order(rh.ORDER_AVX2)
+    dev.state_init(N_PROMPT + N_GEN)
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, N_PROMPT).astype(np.int32)
+    ids0, _ = dev.generate(prompt, N_GEN)  # warm-up (graph capture, first touch)
+    ids, (p_ms, g_ms) = dev.generate(prompt, N_GEN)
+    assert ids == ids0, "generate is not deterministic"
+    assert len(ids) == N_GEN and all(0 <= t < cfg.vocab for t in ids)
+    D_, hd = cfg.dim, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    esz = 2
+    per_layer = (qd + 2 * kvd) * D_ * esz + D_ * qd * esz + cfg.n_experts * D_ * esz + \
+        cfg.top_k * 3 * cfg.expert_hidden * D_ * esz
+    w_bytes = cfg.n_layers * per_layer + cfg.vocab * D_ * esz + D_ * esz
+    mean_pos = N_PROMPT + (N_GEN - 1) / 2.0
+    kv_bytes = cfg.n_layers * 2 * kvd * 4 * mean_pos
+    gen_tok_s = (N_GEN - 1) / (g_ms * 1e-3)
+    tok_bytes = w_bytes + kv_bytes
+    res = {
+        "workload": "OLMoE-1B-7B-shaped model (16 layers, hidden 2048, 16 heads x 128, QK-norm, RoPE, 64 experts "
+                    "top-8, SwiGLU 1024, vocab 50304, bf16 ~N(0,0.02)), 128-token random prompt, greedy decode of "
+                    "256 tokens at batch 1 with the KV cache in HBM",
+        "gen_tok_per_s": round(gen_tok_s, 2),
+        "ms_per_token": round(g_ms / (N_GEN - 1), 4),
+        "prompt_tok_per_s": round(N_PROMPT / (p_ms * 1e-3), 2),
+        "bytes_per_token": int(tok_bytes),
+        "hbm_GBps_alg": round(tok_bytes * gen_tok_s / 1e9, 1),
+        "hbm_frac_alg": round(tok_bytes * gen_tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        "launch": "one HIP graph per token (embedding .. argmax, 7 launches per layer + 3)",
+        "setup_s": round(setup_s, 2),
+    }
+    if with_cpu:
+        res["cpu_baseline"] = cpu_full_model(dev, cfg, prompt, cpu_seconds)
+    dev.close()
+    return res
+
+
+def cpu_full_model(dev, cfg, prompt, seconds):
+    """The engine's forward() (the oracle's orc_run, AVX2 order, bitwise the reference) on one host
+    core over a prefix of the prompt, on the same weights read back from HBM."""
+    from oracle import pyoracle as po
+    size = dev.tensor("lm_head")[0] + dev.tensor("lm_head")[1]
+    img = np.empty(size, np.uint8)
+    dev._check(dev.L.rbt_hip_d2h(dev.h, img.ctypes.data_as(C.c_void_p), dev.model_base, size))
+    hdr = np.frombuffer(b"RBT2" + np.uint32(2).tobytes() + bytes(cfg), np.uint8)  # the .rbt2 header (68 bytes)
+    img[:hdr.size] = hdr
+    try:
+        old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {sorted(old)[0]})
+    except (AttributeError, OSError):
+        old = None
+    try:
+        t0 = time.perf_counter()
+        po.run(img, prompt[:1], order=po.ORDER_AVX2, ctx=len(prompt))
+        t1 = time.perf_counter() - t0
+        n = int(max(2, min(len(prompt), seconds / max(t1, 1e-6))))
+        t0 = time.perf_counter()
+        po.run(img, prompt[:n], order=po.ORDER_AVX2, ctx=len(prompt))
+        dt = time.perf_counter() - t0
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"forward() over the first {n} prompt tokens ({dt:.1f} s, one token per call as the engine's "
+                      f"loop); host {cpu_model()}"}
+
 
 
 PREFILL_T = 512
