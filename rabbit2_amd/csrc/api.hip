@@ -322,11 +322,26 @@ int enqueue_step(rbt_hip *h, bool final) {
             STEP_LAUNCH(kProfWo, launch_dense_resid(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
         else
             STEP_LAUNCH(kProfWo, launch_wo(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
-        STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, reinterpret_cast<const float *>(h->model + ly.ffn_norm), D,
-                                                 c.rms_eps, ds.xb));
         rbt_moe_layer ml;
         if (!rbt_hip_layer(h, l, &ml)) return 0;
-        if (!rbt_hip_moe_dev(h, &ml, ds.xb, 1, ds.x, nullptr, ds.routing + (size_t)l * c.top_k, nullptr)) return 0;
+        const float *ffn_norm = reinterpret_cast<const float *>(h->model + ly.ffn_norm);
+        Workspace &w = h->ws;
+        int32_t *routing = ds.routing + (size_t)l * c.top_k;
+        if (h->fused_decode && c.n_experts <= kTopkInGateupMaxE &&
+            experts_decode_supported(c.dtype, 1, c.top_k, D, c.expert_hidden, ml.experts, ml.expert_stride, ds.xb,
+                                     w.hbuf) &&
+            router_norm_supported(h->order, c.dtype, 1, D, ml.router, ds.x, ffn_norm)) {
+            // the MoE block in three launches with the RMSNorm inside the router kernel (it also writes xb)
+            STEP_LAUNCH(kProfRouter, launch_router_norm(L, ds.x, ffn_norm, c.rms_eps, ml.router, nullptr, 1,
+                                                        c.n_experts, D, w.probs, ds.xb));
+            HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), c.dtype, ml.experts,
+                                            ml.expert_stride, routing, w.weights, ds.xb, w.hbuf, 1, c.top_k, D,
+                                            c.expert_hidden, ds.x, nullptr, w.probs, c.n_experts, c.norm_topk));
+            if (!prof_collect(h)) return 0;
+        } else {
+            STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, ffn_norm, D, c.rms_eps, ds.xb));
+            if (!rbt_hip_moe_dev(h, &ml, ds.xb, 1, ds.x, nullptr, routing, nullptr)) return 0;
+        }
     }
     if (final) {
         const void *W[3] = {h->model + h->lm_head, nullptr, nullptr};

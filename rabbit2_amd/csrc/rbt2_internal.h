@@ -98,6 +98,12 @@ hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype
                          const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,
                          int32_t *routing, float *weights);
 
+// Router logits (AVX2 order, few tokens, bf16) with the RMSNorm in front folded in: x [T][D] is the
+// residual stream and nw the norm weights; token t's xb = x * inv * nw also goes to xb_out [T][D].
+bool router_norm_supported(int order, int dtype, int T, int D, const void *W, const float *x, const float *nw);
+hipError_t launch_router_norm(const Launch &L, const float *x, const float *nw, float eps, const void *W,
+                              const float *bias, int T, int E, int D, float *logits, float *xb_out);
+
 // Only the logits kernel of launch_router.
 hipError_t launch_router_logits(const Launch &L, int order, int dtype, const float *xb, const void *W,
                                 const float *bias, int T, int E, int D, float *logits);

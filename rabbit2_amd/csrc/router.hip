@@ -193,11 +193,15 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 // the row) and transposes them in registers (v_perm pairs the 16-bit halves) into eight 16-byte
 // LDS stores. The 16 chains of a row sit in 16 consecutive lanes: (chain j) + (chain 8+j) via a
 // DPP row rotation, then the sequential sum over j, as the engine's lanes a[j] + b[j].
+// NORM: the kernel also runs the RMSNorm in front of the router (rabbit2.c:512): x is the residual
+// stream, xb = x * inv * nw with inv = 1/sqrtf(sum x^2 / D + eps) from the block's own staging loads,
+// and block (0, t) writes token t's xb to xb_out for the expert kernels.
 constexpr int kDRows = 4;
-template <int M>  // steps per chain = D / 16, a multiple of 8
+template <int M, bool NORM = false>  // steps per chain = D / 16, a multiple of 8
 __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restrict__ xb, const uint16_t *__restrict__ W,
                                                           const float *__restrict__ bias, int E,
-                                                          float *__restrict__ logits) {
+                                                          float *__restrict__ logits, const float *__restrict__ nw = nullptr,
+                                                          float eps = 0.0f, float *__restrict__ xb_out = nullptr) {
     constexpr int D = 16 * M;
     constexpr int WP = M + 8;  // bf16 per (row, chain) line: 16-byte pad, lanes of one read hit distinct banks
     constexpr int XP = M + 4;  // f32 per chain line
@@ -231,6 +235,42 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
             const float *src = x + 16 * (8 * g + i) + 8 * h;
             xv[q][i][0] = *reinterpret_cast<const f32x4 *>(src);
             xv[q][i][1] = *reinterpret_cast<const f32x4 *>(src + 4);
+        }
+    }
+    if constexpr (NORM) {
+        // sum of squares over the token's x (every element once: tasks past XT repeat the last one)
+        float ss = 0.0f;
+#pragma unroll
+        for (int q = 0; q < XPER; ++q) {
+            if (tid + 64 * q < XT) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        ss += xv[q][i][j].x * xv[q][i][j].x + xv[q][i][j].y * xv[q][i][j].y +
+                              xv[q][i][j].z * xv[q][i][j].z + xv[q][i][j].w * xv[q][i][j].w;
+            }
+        }
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int q = 0; q < XPER; ++q) {
+            const int task = min(tid + 64 * q, XT - 1);
+            const int h = task / G, g = task % G;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int off = 16 * (8 * g + i) + 8 * h;
+                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(nw + off);
+                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(nw + off + 4);
+                f32x4 &a = xv[q][i][0], &b = xv[q][i][1];
+                a = f32x4{a.x * inv * w0.x, a.y * inv * w0.y, a.z * inv * w0.z, a.w * inv * w0.w};
+                b = f32x4{b.x * inv * w1.x, b.y * inv * w1.y, b.z * inv * w1.z, b.w * inv * w1.w};
+                if (blockIdx.x == 0 && tid + 64 * q < XT) {
+                    float *dst = xb_out + (size_t)t * D + off;
+                    *reinterpret_cast<f32x4 *>(dst) = a;
+                    *reinterpret_cast<f32x4 *>(dst + 4) = b;
+                }
+            }
         }
     }
     // transposed stores (clamped tasks rewrite the last task's identical data)
@@ -736,22 +776,33 @@ inline bool decode_ok(int T, int D, int dtype, const void *W, const float *xb) {
            (reinterpret_cast<uintptr_t>(xb) % 16 == 0);
 }
 
-inline hipError_t launch_router_decode(const Launch &L, const float *xb, const void *W, const float *bias, int T, int E,
-                                       int D, float *logits) {
+template <bool NORM>
+inline hipError_t launch_router_decode_t(const Launch &L, const float *xb, const void *W, const float *bias, int T,
+                                         int E, int D, float *logits, const float *nw, float eps, float *xb_out) {
     const dim3 g((unsigned)((E + kDRows - 1) / kDRows), (unsigned)T), b(64);
     const uint16_t *w = static_cast<const uint16_t *>(W);
     switch (D / 16) {
-        case 8: return launch(L, router_decode_kernel<8>, g, b, 0, xb, w, bias, E, logits);
-        case 16: return launch(L, router_decode_kernel<16>, g, b, 0, xb, w, bias, E, logits);
-        case 32: return launch(L, router_decode_kernel<32>, g, b, 0, xb, w, bias, E, logits);
-        case 48: return launch(L, router_decode_kernel<48>, g, b, 0, xb, w, bias, E, logits);
-        case 64: return launch(L, router_decode_kernel<64>, g, b, 0, xb, w, bias, E, logits);
-        case 96: return launch(L, router_decode_kernel<96>, g, b, 0, xb, w, bias, E, logits);
-        case 128: return launch(L, router_decode_kernel<128>, g, b, 0, xb, w, bias, E, logits);
-        case 192: return launch(L, router_decode_kernel<192>, g, b, 0, xb, w, bias, E, logits);
-        case 256: return launch(L, router_decode_kernel<256>, g, b, 0, xb, w, bias, E, logits);
-        default: return hipErrorNotSupported;
+#define RD_CASE(m) \
+    case m:        \
+        return launch(L, router_decode_kernel<m, NORM>, g, b, 0, xb, w, bias, E, logits, nw, eps, xb_out);
+        RD_CASE(8)
+        RD_CASE(16)
+        RD_CASE(32)
+        RD_CASE(48)
+        RD_CASE(64)
+        RD_CASE(96)
+        RD_CASE(128)
+        RD_CASE(192)
+        RD_CASE(256)
+#undef RD_CASE
+        default:
+            return hipErrorNotSupported;
     }
+}
+
+inline hipError_t launch_router_decode(const Launch &L, const float *xb, const void *W, const float *bias, int T, int E,
+                                       int D, float *logits) {
+    return launch_router_decode_t<false>(L, xb, W, bias, T, E, D, logits, nullptr, 0.0f, nullptr);
 }
 
 // The batch kernel (AVX2 order) from 16 tokens on; its 16-byte staging needs 16-byte aligned rows.
@@ -810,6 +861,15 @@ hipError_t launch_router_logits(const Launch &L, int order, int dtype, const flo
     }
     return dtype == RBT_DT_BF16 ? launch_logits<4, RBT_DT_BF16, false>(L, xb, W, bias, T, E, D, 64, logits)
                                 : launch_logits<4, RBT_DT_F32, false>(L, xb, W, bias, T, E, D, 64, logits);
+}
+
+bool router_norm_supported(int order, int dtype, int T, int D, const void *W, const float *x, const float *nw) {
+    return order == RBT_ORDER_AVX2 && decode_ok(T, D, dtype, W, x) && (reinterpret_cast<uintptr_t>(nw) & 15u) == 0;
+}
+
+hipError_t launch_router_norm(const Launch &L, const float *x, const float *nw, float eps, const void *W,
+                              const float *bias, int T, int E, int D, float *logits, float *xb_out) {
+    return launch_router_decode_t<true>(L, x, W, bias, T, E, D, logits, nw, eps, xb_out);
 }
 
 bool router_prefill_supported(int order, int dtype, int T, int E, int D, int K, const void *W, const float *xb) {
