@@ -77,6 +77,16 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
  * replaces the engine's get_expert() streaming and LRU cache (rabbit2.c:233-300): 16 x 64 OLMoE
  * experts are 12 GiB of the 288 GB HBM. Fills *cfg (may be NULL). */
 int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config *cfg);
+/* The same from a file path: reads the header and validates it like load_model (rabbit2.c:199-228),
+ * maps the file read-only and copies the image to HBM once, sequentially (replaces map_file and
+ * get_expert's reads, rabbit2.c:129-156, :261-300). Fills *cfg (may be NULL). */
+int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg);
+/* The engine's expert-cache counters (rabbit2.c:745-751) for the HBM-resident image:
+ * stats = {hits, misses, evictions, bytes_read, resident_bytes, capacity_bytes}. Every expert is a
+ * miss once (read at upload) and stays resident: evictions 0, bytes_read = misses * expert_stride,
+ * capacity = resident = all experts; hits counts the experts selected by the host-pointer calls
+ * (rbt_hip_moe, rbt_hip_forward), whose routing passes through the host. */
+int rbt_hip_expert_stats(rbt_hip *h, uint64_t stats[6]);
 /* Device view of layer `layer` of the uploaded model (for the _dev calls). */
 int rbt_hip_layer(rbt_hip *h, int layer, rbt_moe_layer *out);
 

@@ -21,7 +21,7 @@ EXPORTS = (
     "rbt_hip_matvec", "rbt_hip_matvec_dev", "rbt_hip_malloc", "rbt_hip_free_dev", "rbt_hip_h2d", "rbt_hip_d2h",
     "rbt_hip_memset_dev", "rbt_hip_synchronize", "rbt_hip_stream", "rbt_hip_fill_normal", "rbt_hip_profile_enable",
     "rbt_hip_profile_get", "rbt_hip_set_option", "rbt_hip_state_init", "rbt_hip_forward", "rbt_hip_generate",
-    "rbt_hip_model_create", "rbt_hip_tensor",
+    "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats",
 )
 
 
@@ -81,6 +81,8 @@ def lib():
         L.rbt_hip_generate.argtypes = [vp, vp, i32, i32, C.c_int32, vp, C.POINTER(C.c_int), C.POINTER(C.c_double)]
         L.rbt_hip_model_create.argtypes = [vp, C.POINTER(Config), C.POINTER(vp)]
         L.rbt_hip_tensor.argtypes = [vp, C.c_char_p, i32, C.POINTER(u64), C.POINTER(u64)]
+        L.rbt_hip_upload_file.argtypes = [vp, C.c_char_p, C.POINTER(Config)]
+        L.rbt_hip_expert_stats.argtypes = [vp, C.POINTER(C.c_uint64)]
         _lib = L
     return _lib
 
@@ -197,6 +199,17 @@ class Device:
         cfg = Config()
         self._check(self.L.rbt_hip_upload(self.h, _p(model), model.size, C.byref(cfg)))
         return cfg
+
+    def upload_file(self, path):
+        cfg = Config()
+        self._check(self.L.rbt_hip_upload_file(self.h, os.fsencode(path), C.byref(cfg)))
+        return cfg
+
+    def expert_stats(self):
+        """{hits, misses, evictions, bytes_read, resident_bytes, capacity_bytes}"""
+        a = (C.c_uint64 * 6)()
+        self._check(self.L.rbt_hip_expert_stats(self.h, a))
+        return dict(zip(("hits", "misses", "evictions", "bytes_read", "resident_bytes", "capacity_bytes"), a))
 
     def layer(self, l):
         L = MoeLayer()
