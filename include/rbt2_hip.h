@@ -142,6 +142,20 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
 int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
                      int *n_out, double *ms_out);
 
+/* ---- batched decode (no counterpart in the reference, whose State holds one sequence): n_seq
+ * independent sequences stepped together, each with its own KV cache of ctx positions. Every weight is
+ * read once per step for all of them: the dense matvecs run over the n_seq token vectors, and the MoE
+ * block takes the n_seq tokens as one batch (the grouped path from "prefill_min_tokens" tokens on). */
+int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx);
+/* One forward() per sequence: sequence b takes tokens[b] at position pos[b] (positions advance
+ * independently, in order per sequence). logits [n_seq][vocab], routing_out [n_layers][n_seq][top_k]
+ * (either may be NULL). Synchronous. */
+int rbt_hip_forward_batch(rbt_hip *h, const int32_t *tokens, const int32_t *pos, float *logits, int32_t *routing_out);
+/* Greedy --gen for every sequence on the device: prompts [n_seq][n_prompt] from position 0, then
+ * n_gen tokens each (at most ctx - n_prompt) into out [n_seq][n_gen]; one graph replay per step for
+ * all sequences. ms_out (may be NULL): [prompt ms, generation ms]. */
+int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int n_gen, int32_t *out, double *ms_out);
+
 /* A model image built in place on the device instead of uploaded (no counterpart in the reference,
  * whose synthetic models are written to files by rabbit2/ref/rbt2.py): validates cfg like
  * rbt_hip_upload, allocates the image with the file layout (rabbit2.c:158-193) and returns its device
@@ -166,7 +180,7 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
  * stream and its duration is accumulated under its name ("router", "topk", "gateup",
  * "down_combine"; the grouped path adds "dispatch" -- the activation hi/lo split and the per-expert
  * lists -- and "combine", and its "down_combine" is the down GEMM alone); rbt_hip_forward adds
- * "embed", "qkv" (RMSNorm + q/k/v), "attention", "attn_merge", "wo", "ffn_norm", "lm_head" (final
+ * "embed", "attn_norm", "qkv" (RMSNorm + q/k/v), "attention", "attn_merge", "wo", "ffn_norm", "lm_head" (final
  * norm + lm_head, with the argmax inside where the rows allow) and "argmax" (otherwise). Each timed launch then waits for its own work (rbt_hip_generate
  * is never timed this way). rbt_hip_profile_get returns 0 for an unknown name. Meant for
  * measurement passes, not for the timed hot loop. */

@@ -34,10 +34,11 @@ struct LayerOff {
 enum ProfKernel {
     kProfRouter, kProfTopk, kProfGateup, kProfDown, kProfDispatch, kProfCombine,
     // the rest of the forward pass (rbt_hip_forward with profiling on)
-    kProfEmbed, kProfQkv, kProfAttn, kProfAttnMerge, kProfWo, kProfFfnNorm, kProfLmHead, kProfArgmax, kProfCount
+    kProfEmbed, kProfAttnNorm, kProfQkv, kProfAttn, kProfAttnMerge, kProfWo, kProfFfnNorm, kProfLmHead, kProfArgmax,
+    kProfCount
 };
 const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_combine", "dispatch", "combine",
-                                            "embed", "qkv", "attention", "attn_merge", "wo", "ffn_norm",
+                                            "embed", "attn_norm", "qkv", "attention", "attn_merge", "wo", "ffn_norm",
                                             "lm_head", "argmax"};
 
 struct Profile {
@@ -51,17 +52,18 @@ struct Profile {
 // Decode state of the full forward pass (rbt_hip_state_init): one allocation carved into the KV cache
 // and the per-step buffers.
 struct DecodeState {
+    int n_seq = 0;                // sequences stepped together (1 for the engine's single State)
     int ctx = 0, S = 0;           // context length, attention splits
     uint8_t *block = nullptr;     // the allocation
-    float *kc = nullptr, *vc = nullptr;  // [n_layers][ctx][kv_dim]
+    float *kc = nullptr, *vc = nullptr;  // [n_seq][n_layers][ctx][kv_dim]
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr;
     float *part = nullptr;        // attention split partials [n_heads][S][hd + 2]
     float2 *rope_cs = nullptr;    // [ctx][hd/2] (cos, sin) of the RoPE angles
     float2 *cand = nullptr;       // lm_head blocks' argmax candidates
     float *logits = nullptr;      // [vocab]
-    int32_t *routing = nullptr;   // [n_layers][top_k]
-    int32_t *seq = nullptr;       // [ctx] token of each position
-    StepState *st = nullptr;
+    int32_t *routing = nullptr;   // [n_layers][n_seq][top_k]
+    int32_t *seq = nullptr;       // [n_seq][ctx] token of each position
+    StepState *st = nullptr;      // [n_seq]
 };
 
 struct Workspace {
@@ -296,6 +298,7 @@ int model_alloc(rbt_hip *h) {
 int enqueue_step(rbt_hip *h, bool final) {
     const rbt_config &c = h->cfg;
     DecodeState &ds = h->ds;
+    const int B = ds.n_seq;
     const int D = c.dim, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     // with profiling on (eager calls only), every launch is timed by its own event pair and collected
     // right away, since each kernel kind runs once per layer
@@ -305,37 +308,53 @@ int enqueue_step(rbt_hip *h, bool final) {
         HIP_OK(h, (call));                    \
         if (!prof_collect(h)) return 0;       \
     } while (0)
-    STEP_LAUNCH(kProfEmbed, launch_embed(L, c.dtype, h->model + h->tok_emb, D, c.vocab, ds.st, ds.seq, ds.x));
+    STEP_LAUNCH(kProfEmbed, launch_embed(L, c.dtype, h->model + h->tok_emb, D, c.vocab, ds.st, ds.seq, ds.ctx, ds.x, B));
     for (int l = 0; l < c.n_layers; l++) {
         const LayerOff &ly = h->layers[(size_t)l];
         const void *W[3] = {h->model + ly.wq, h->model + ly.wk, h->model + ly.wv};
         float *const out[3] = {ds.q, ds.k, ds.v};
         const int rows[3] = {qd, kvd, kvd};
         const float *attn_norm = reinterpret_cast<const float *>(h->model + ly.attn_norm);
-        if (dense_supported(c.dtype, D, W, rows))
+        const bool dense = dense_supported(c.dtype, D, W, rows);
+        if (B == 1 && dense) {
             STEP_LAUNCH(kProfQkv, launch_dense_norm(L, c.dtype, ds.x, attn_norm, c.rms_eps, D, W, out, rows));
-        else
-            STEP_LAUNCH(kProfQkv, launch_norm_matvec(L, c.dtype, ds.x, attn_norm, c.rms_eps, D, W, out, rows));
-        const size_t cache = (size_t)l * ds.ctx * kvd;
+        } else if (dense) {  // batched: the norm once per token, then every weight read once for all tokens
+            STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B));
+            STEP_LAUNCH(kProfQkv, launch_dense_batch(L, c.dtype, ds.xb, B, D, W, out, rows, nullptr));
+        } else {
+            for (int b = 0; b < B; b++) {
+                float *const ob[3] = {ds.q + (size_t)b * qd, ds.k + (size_t)b * kvd, ds.v + (size_t)b * kvd};
+                STEP_LAUNCH(kProfQkv, launch_norm_matvec(L, c.dtype, ds.x + (size_t)b * D, attn_norm, c.rms_eps, D,
+                                                         W, ob, rows));
+            }
+        }
+        const size_t cache = (size_t)l * ds.ctx * kvd, seq_stride = (size_t)c.n_layers * ds.ctx * kvd;
         STEP_LAUNCH(kProfAttn,
                     launch_attention(L, ds.q, ds.k, ds.v,
                                      c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.q_norm) : ds.q,
                                      c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.k_norm) : ds.k,
                                      c.qk_norm, c.rms_eps, c.n_heads, c.n_kv_heads, hd, ds.S, ds.st, ds.kc + cache,
-                                     ds.vc + cache, ds.rope_cs, ds.part));
+                                     ds.vc + cache, seq_stride, ds.rope_cs, ds.part, B));
+        STEP_LAUNCH(kProfAttnMerge, launch_attn_merge(L, ds.part, c.n_heads, hd, ds.S, ds.ao, B));
         const void *Wo[3] = {h->model + ly.wo, nullptr, nullptr};
+        float *const no_out[3] = {nullptr, nullptr, nullptr};
         const int wo_rows[3] = {D, 0, 0};
-        STEP_LAUNCH(kProfAttnMerge, launch_attn_merge(L, ds.part, c.n_heads, hd, ds.S, ds.ao));
-        if (dense_supported(c.dtype, qd, Wo, wo_rows))
-            STEP_LAUNCH(kProfWo, launch_dense_resid(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
-        else
-            STEP_LAUNCH(kProfWo, launch_wo(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
+        if (dense_supported(c.dtype, qd, Wo, wo_rows)) {
+            if (B == 1)
+                STEP_LAUNCH(kProfWo, launch_dense_resid(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
+            else
+                STEP_LAUNCH(kProfWo, launch_dense_batch(L, c.dtype, ds.ao, B, qd, Wo, no_out, wo_rows, ds.x));
+        } else {
+            for (int b = 0; b < B; b++)
+                STEP_LAUNCH(kProfWo, launch_wo(L, c.dtype, ds.ao + (size_t)b * qd, qd, h->model + ly.wo, D,
+                                               ds.x + (size_t)b * D));
+        }
         rbt_moe_layer ml;
         if (!rbt_hip_layer(h, l, &ml)) return 0;
         const float *ffn_norm = reinterpret_cast<const float *>(h->model + ly.ffn_norm);
         Workspace &w = h->ws;
-        int32_t *routing = ds.routing + (size_t)l * c.top_k;
-        if (h->fused_decode && c.n_experts <= kTopkInGateupMaxE &&
+        int32_t *routing = ds.routing + (size_t)l * B * c.top_k;
+        if (B == 1 && h->fused_decode && c.n_experts <= kTopkInGateupMaxE &&
             experts_decode_supported(c.dtype, 1, c.top_k, D, c.expert_hidden, ml.experts, ml.expert_stride, ds.xb,
                                      w.hbuf) &&
             router_norm_supported(h->order, c.dtype, 1, D, ml.router, ds.x, ffn_norm)) {
@@ -347,8 +366,8 @@ int enqueue_step(rbt_hip *h, bool final) {
                                             c.expert_hidden, ds.x, nullptr, w.probs, c.n_experts, c.norm_topk));
             if (!prof_collect(h)) return 0;
         } else {
-            STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, ffn_norm, D, c.rms_eps, ds.xb));
-            if (!rbt_hip_moe_dev(h, &ml, ds.xb, 1, ds.x, nullptr, routing, nullptr)) return 0;
+            STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, ffn_norm, D, c.rms_eps, ds.xb, B));
+            if (!rbt_hip_moe_dev(h, &ml, ds.xb, B, ds.x, nullptr, routing, nullptr)) return 0;
         }
     }
     if (final) {
@@ -356,15 +375,25 @@ int enqueue_step(rbt_hip *h, bool final) {
         float *const out[3] = {ds.logits, nullptr, nullptr};
         const int rows[3] = {c.vocab, 0, 0};
         const float *fn = reinterpret_cast<const float *>(h->model + h->final_norm);
-        if (dense_supported(c.dtype, D, W, rows)) {  // lm_head and the argmax in one launch
+        const bool dense = dense_supported(c.dtype, D, W, rows);
+        if (B == 1 && dense) {  // lm_head with per-block argmax candidates, then the argmax
             STEP_LAUNCH(kProfLmHead, launch_dense_argmax(L, c.dtype, ds.x, fn, c.rms_eps, D, W[0], c.vocab, ds.logits,
                                                          ds.cand, ds.st, ds.seq, ds.ctx));
         } else {
-            STEP_LAUNCH(kProfLmHead, launch_norm_matvec(L, c.dtype, ds.x, fn, c.rms_eps, D, W, out, rows));
-            STEP_LAUNCH(kProfArgmax, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx));
+            if (dense) {
+                STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B));
+                STEP_LAUNCH(kProfLmHead, launch_dense_batch(L, c.dtype, ds.xb, B, D, W, out, rows, nullptr));
+            } else {
+                for (int b = 0; b < B; b++) {
+                    float *const ob[3] = {ds.logits + (size_t)b * c.vocab, nullptr, nullptr};
+                    STEP_LAUNCH(kProfLmHead, launch_norm_matvec(L, c.dtype, ds.x + (size_t)b * D, fn, c.rms_eps, D, W,
+                                                                ob, rows));
+                }
+            }
+            STEP_LAUNCH(kProfArgmax, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx, B));
         }
     } else {
-        STEP_LAUNCH(-1, launch_advance(L, ds.st));
+        STEP_LAUNCH(-1, launch_advance(L, ds.st, B));
     }
 #undef STEP_LAUNCH
     return 1;
@@ -829,11 +858,14 @@ int rbt_hip_fill_normal(rbt_hip *h, void *dst_dev, int dtype, uint64_t n, uint64
     return 1;
 }
 
-int rbt_hip_state_init(rbt_hip *h, int ctx) {
+int rbt_hip_state_init(rbt_hip *h, int ctx) { return rbt_hip_batch_init(h, 1, ctx); }
+
+int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     if (!h) return fail(nullptr, "state_init: handle is NULL");
     if (!h->model) return fail(h, "state_init: no model");
     const rbt_config &c = h->cfg;
     if (ctx < 0) return fail(h, "state_init: negative context");
+    if (n_seq < 1 || n_seq > 1024) return fail(h, "state_init: n_seq must be in [1, 1024]");
     if (ctx == 0) ctx = c.max_seq < 512 ? c.max_seq : 512;  // rabbit2.c:684
     if (ctx > c.max_seq) ctx = c.max_seq;                   // rabbit2.c:685
     if (!set_device(h)) return 0;
@@ -841,6 +873,7 @@ int rbt_hip_state_init(rbt_hip *h, int ctx) {
     (void)hipFree(h->ds.block);
     h->ds = DecodeState{};
     DecodeState ds;
+    ds.n_seq = n_seq;
     ds.ctx = ctx;
     ds.S = ctx / 32 < 1 ? 1 : (ctx / 32 > 16 ? 16 : ctx / 32);  // attention splits over positions (<= 64)
     const uint64_t D = (uint64_t)c.dim, hd = (uint64_t)c.head_dim, qd = (uint64_t)c.n_heads * hd,
@@ -851,14 +884,15 @@ int rbt_hip_state_init(rbt_hip *h, int ctx) {
         off = align_up(off + bytes, 256);
         return at;
     };
-    const uint64_t o_kc = carve(4 * (uint64_t)c.n_layers * ctx * kvd), o_vc = carve(4 * (uint64_t)c.n_layers * ctx * kvd);
-    const uint64_t o_x = carve(4 * D), o_xb = carve(4 * D), o_q = carve(4 * qd), o_k = carve(4 * kvd),
-                   o_v = carve(4 * kvd), o_ao = carve(4 * qd);
-    const uint64_t o_part = carve(4 * (uint64_t)c.n_heads * ds.S * (hd + 2));
+    const uint64_t B = (uint64_t)n_seq;
+    const uint64_t o_kc = carve(4 * B * c.n_layers * ctx * kvd), o_vc = carve(4 * B * c.n_layers * ctx * kvd);
+    const uint64_t o_x = carve(4 * B * D), o_xb = carve(4 * B * D), o_q = carve(4 * B * qd), o_k = carve(4 * B * kvd),
+                   o_v = carve(4 * B * kvd), o_ao = carve(4 * B * qd);
+    const uint64_t o_part = carve(4 * B * c.n_heads * ds.S * (hd + 2));
     const uint64_t o_rope = carve(8 * (uint64_t)ctx * (hd / 2));
     const uint64_t o_cand = carve(8 * (uint64_t)dense_argmax_blocks(c.vocab));
-    const uint64_t o_lg = carve(4 * (uint64_t)c.vocab), o_rt = carve(4 * (uint64_t)c.n_layers * c.top_k);
-    const uint64_t o_seq = carve(4 * (uint64_t)ctx), o_st = carve(sizeof(StepState));
+    const uint64_t o_lg = carve(4 * B * c.vocab), o_rt = carve(4 * B * c.n_layers * c.top_k);
+    const uint64_t o_seq = carve(4 * B * ctx), o_st = carve(sizeof(StepState) * B);
     if (c.head_dim > 256 || 4 * D > 64 * 1024 || 4 * qd > 64 * 1024)
         return fail(h, "state_init: head_dim above 256 or dim above 16384 is not supported");
     HIP_OK(h, hipMalloc(&ds.block, off));
@@ -897,15 +931,16 @@ int rbt_hip_state_init(rbt_hip *h, int ctx) {
         }
     }
     h->ds = ds;
-    // the MoE workspace for one token per layer call, so that no step allocates
+    // the MoE workspace for n_seq tokens per layer call, so that no step allocates
     rbt_moe_layer ml;
-    if (!rbt_hip_layer(h, 0, &ml) || !rbt_hip_reserve(h, &ml, 1)) return 0;
+    if (!rbt_hip_layer(h, 0, &ml) || !rbt_hip_reserve(h, &ml, n_seq)) return 0;
     return 1;
 }
 
 int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *routing_out) {
     if (!h) return fail(nullptr, "forward: handle is NULL");
     if (!h->ds.block) return fail(h, "forward: no decode state (rbt_hip_state_init)");
+    if (h->ds.n_seq != 1) return fail(h, "forward: the state holds %d sequences (rbt_hip_forward_batch)", h->ds.n_seq);
     const rbt_config &c = h->cfg;
     if (token < 0 || token >= c.vocab) return fail(h, "token %d out of range", token);
     if (pos < 0 || pos >= h->ds.ctx) return fail(h, "forward: position %d outside the context of %d", pos, h->ds.ctx);
@@ -928,6 +963,7 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
     if (!h) return fail(nullptr, "generate: handle is NULL");
     if (n_out) *n_out = 0;
     if (!h->ds.block) return fail(h, "generate: no decode state (rbt_hip_state_init)");
+    if (h->ds.n_seq != 1) return fail(h, "generate: the state holds %d sequences (rbt_hip_generate_batch)", h->ds.n_seq);
     const rbt_config &c = h->cfg;
     const int ctx = h->ds.ctx;
     if (!prompt || n_prompt < 1) return fail(h, "generate: empty prompt");
@@ -987,6 +1023,89 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
             break;
         }
     if (n_out) *n_out = n;
+    return 1;
+}
+
+int rbt_hip_forward_batch(rbt_hip *h, const int32_t *tokens, const int32_t *pos, float *logits, int32_t *routing_out) {
+    if (!h) return fail(nullptr, "forward_batch: handle is NULL");
+    if (!h->ds.block) return fail(h, "forward_batch: no decode state (rbt_hip_batch_init)");
+    if (!tokens || !pos) return fail(h, "forward_batch: NULL argument");
+    const rbt_config &c = h->cfg;
+    const int B = h->ds.n_seq;
+    std::vector<StepState> st((size_t)B);
+    for (int b = 0; b < B; b++) {
+        if (tokens[b] < 0 || tokens[b] >= c.vocab) return fail(h, "token %d out of range", tokens[b]);
+        if (pos[b] < 0 || pos[b] >= h->ds.ctx)
+            return fail(h, "forward_batch: position %d outside the context of %d", pos[b], h->ds.ctx);
+        st[(size_t)b] = StepState{pos[b], 0x7FFFFFFF, 0, 0};
+    }
+    if (!set_device(h)) return 0;
+    for (int b = 0; b < B; b++)
+        HIP_OK(h, hipMemcpyAsync(h->ds.seq + (size_t)b * h->ds.ctx + pos[b], tokens + b, 4, hipMemcpyHostToDevice,
+                                 h->stream));
+    HIP_OK(h, hipMemcpyAsync(h->ds.st, st.data(), sizeof(StepState) * B, hipMemcpyHostToDevice, h->stream));
+    if (!enqueue_step(h, true)) return 0;
+    if (logits)
+        HIP_OK(h, hipMemcpyAsync(logits, h->ds.logits, 4 * (size_t)B * c.vocab, hipMemcpyDeviceToHost, h->stream));
+    if (routing_out)
+        HIP_OK(h, hipMemcpyAsync(routing_out, h->ds.routing, 4 * (size_t)c.n_layers * B * c.top_k,
+                                 hipMemcpyDeviceToHost, h->stream));
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    h->cache_hits += (uint64_t)c.n_layers * B * c.top_k;
+    return 1;
+}
+
+int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int n_gen, int32_t *out, double *ms_out) {
+    if (!h) return fail(nullptr, "generate_batch: handle is NULL");
+    if (!h->ds.block) return fail(h, "generate_batch: no decode state (rbt_hip_batch_init)");
+    const rbt_config &c = h->cfg;
+    const int B = h->ds.n_seq, ctx = h->ds.ctx;
+    if (!prompts || n_prompt < 1) return fail(h, "generate_batch: empty prompts");
+    if (n_prompt > ctx) return fail(h, "prompt has %d tokens but context is %d (use --ctx)", n_prompt, ctx);
+    for (size_t i = 0; i < (size_t)B * n_prompt; i++)
+        if (prompts[i] < 0 || prompts[i] >= c.vocab) return fail(h, "token %d out of range", prompts[i]);
+    if (n_gen < 0 || n_gen > ctx - n_prompt)
+        return fail(h, "generate_batch: n_gen %d outside [0, ctx - n_prompt = %d]", n_gen, ctx - n_prompt);
+    if (n_gen > 0 && !out) return fail(h, "generate_batch: out is NULL");
+    if (!set_device(h)) return 0;
+    std::vector<StepState> st((size_t)B, StepState{0, n_prompt, 0, 0});
+    for (int b = 0; b < B; b++)
+        HIP_OK(h, hipMemcpyAsync(h->ds.seq + (size_t)b * ctx, prompts + (size_t)b * n_prompt, 4 * (size_t)n_prompt,
+                                 hipMemcpyHostToDevice, h->stream));
+    HIP_OK(h, hipMemcpyAsync(h->ds.st, st.data(), sizeof(StepState) * B, hipMemcpyHostToDevice, h->stream));
+    const bool prof = h->prof.on;
+    h->prof.on = false;
+    hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    int ok = capture_step(h, false, &g_adv) && capture_step(h, true, &g_fin);
+    h->prof.on = prof;
+    hipError_t e = hipSuccess;
+    if (ok) {
+        for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);
+        if (e == hipSuccess) e = hipEventRecord(ev[0], h->stream);
+        for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = hipGraphLaunch(g_adv, h->stream);
+        if (e == hipSuccess && n_gen > 0) e = hipGraphLaunch(g_fin, h->stream);
+        if (e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
+        for (int g = 1; g < n_gen && e == hipSuccess; g++) e = hipGraphLaunch(g_fin, h->stream);
+        if (e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+        for (int b = 0; b < B && e == hipSuccess && n_gen > 0; b++)
+            e = hipMemcpyAsync(out + (size_t)b * n_gen, h->ds.seq + (size_t)b * ctx + n_prompt, 4 * (size_t)n_gen,
+                               hipMemcpyDeviceToHost, h->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+        if (e == hipSuccess && ms_out) {
+            float a = 0.0f, bms = 0.0f;
+            e = hipEventElapsedTime(&a, ev[0], ev[1]);
+            if (e == hipSuccess) e = hipEventElapsedTime(&bms, ev[1], ev[2]);
+            ms_out[0] = a;
+            ms_out[1] = bms;
+        }
+    }
+    if (g_adv) (void)hipGraphExecDestroy(g_adv);
+    if (g_fin) (void)hipGraphExecDestroy(g_fin);
+    for (hipEvent_t ei : ev)
+        if (ei) (void)hipEventDestroy(ei);
+    if (!ok) return 0;
+    if (e != hipSuccess) return fail(h, "generate_batch: %s", hipGetErrorString(e));
     return 1;
 }
 

@@ -5,7 +5,9 @@
 //
 // Every kernel reads the token and position of the step from a small device record (StepState), so
 // one captured step replays unchanged for every position: the prompt's tokens sit in seq[] before the
-// first step, and the argmax kernel appends each generated token to seq[] and advances pos.
+// first step, and the argmax kernel appends each generated token to seq[] and advances pos. A step can
+// carry B independent sequences (batched decode): the per-token kernels take the sequence from a grid
+// dimension, each sequence with its own record, token row seq[b][ctx] and KV cache.
 //
 // Arithmetic follows the engine's formulas (rmsnorm as x * inv * w with inv = 1/sqrtf(ss/n + eps);
 // RoPE angles in double, rounded to float; softmax with max-subtract and expf; strict '>' argmax). Sums
@@ -72,10 +74,11 @@ __device__ __forceinline__ float row_dot(const uint8_t *__restrict__ row, const 
 template <int DT>
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ emb, int D, int vocab,
                                                     const StepState *__restrict__ st, const int32_t *__restrict__ seq,
-                                                    float *__restrict__ x) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+                                                    int ctx, float *__restrict__ x) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
     if (i >= D) return;
-    int tok = seq[st->pos];
+    x += (size_t)b * D;
+    int tok = seq[(size_t)b * ctx + st[b].pos];
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);  // ids are checked on the host; generated ids are in range
     x[i] = elem<DT>(emb, (size_t)tok * D + i);
 }
@@ -213,6 +216,75 @@ __global__ __launch_bounds__(256) void dense_kernel(const float *__restrict__ x,
     }
 }
 
+// ---------------------------------------------------------------- dense matvec over B tokens
+// The rows of dense_kernel for B token vectors (batched decode): each wave keeps its RPW rows' weights
+// in registers, and the B input rows pass through LDS TB at a time, so every weight is read from HBM
+// once per step whatever B is.
+//   MODE 0: out_s[b * rows_s + r] = W_s[r] . xin[b]     (q/k/v, lm_head)
+//   MODE 1: resid[b * total_rows + r] += W[r] . xin[b]   (wo + residual)
+template <int DT, int NC, int RPW, int MODE>
+__global__ __launch_bounds__(256) void dense_batch_kernel(const float *__restrict__ xin, int B, Segs sg, int total_rows,
+                                                          float *__restrict__ resid) {
+    constexpr int kPer = DT == RBT_DT_BF16 ? 8 : 4, kEsz = DT == RBT_DT_BF16 ? 2 : 4;
+    constexpr int D = NC * kWave * kPer;
+    constexpr int TB = 16384 / D < 16 ? 16384 / D : 16;  // 64 KiB of LDS
+    __shared__ __align__(16) float xs[TB * D];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int r0 = (blockIdx.x * 4 + wv) * RPW;
+    u32x4 w[RPW][NC];
+    int seg[RPW], row[RPW];
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        int r = min(r0 + j, total_rows - 1), s = 0;
+        while (s < 2 && r >= sg.rows[s]) {
+            r -= sg.rows[s];
+            ++s;
+        }
+        seg[j] = s;
+        row[j] = r;
+        const uint8_t *src = sg.W[s] + (size_t)r * D * kEsz;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) w[j][i] = ld_stream_u4(src + (size_t)(lane + kWave * i) * 16);
+    }
+    for (int b0 = 0; b0 < B; b0 += TB) {  // block-uniform
+        const int nb = B - b0 < TB ? B - b0 : TB;
+        __syncthreads();  // the previous chunk's reads are done
+        for (int i = threadIdx.x; i < nb * D; i += blockDim.x) xs[i] = xin[(size_t)b0 * D + i];
+        __syncthreads();
+        for (int tt = 0; tt < nb; ++tt) {
+            const float *xt = xs + tt * D;
+#pragma unroll
+            for (int j = 0; j < RPW; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NC; ++i) {
+                    const float *xp = xt + (lane + kWave * i) * kPer;
+                    const u32x4 v = w[j][i];
+                    if constexpr (DT == RBT_DT_BF16) {
+                        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xp), x1 = *reinterpret_cast<const f32x4 *>(xp + 4);
+                        acc += bf16_lo(v.x) * x0.x + bf16_hi(v.x) * x0.y + bf16_lo(v.y) * x0.z + bf16_hi(v.y) * x0.w +
+                               bf16_lo(v.z) * x1.x + bf16_hi(v.z) * x1.y + bf16_lo(v.w) * x1.z + bf16_hi(v.w) * x1.w;
+                    } else {
+                        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xp);
+                        acc += __uint_as_float(v.x) * x0.x + __uint_as_float(v.y) * x0.y +
+                               __uint_as_float(v.z) * x0.z + __uint_as_float(v.w) * x0.w;
+                    }
+                }
+                const float sum = wave_sum(acc);
+                if (lane == 0 && r0 + j < total_rows) {
+                    const size_t b = (size_t)(b0 + tt);
+                    if constexpr (MODE == 1) {
+                        float *o = resid + b * total_rows + row[j];
+                        *o = *o + sum;
+                    } else {
+                        sg.out[seg[j]][b * sg.rows[seg[j]] + row[j]] = sum;
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Greedy argmax over the lm_head blocks' candidates (value, first index; index -1 = none), then the step
 // advances like argmax_kernel: the engine's scan keeps index 0 when logits[0] is NaN or nothing beats it.
 __global__ __launch_bounds__(1024) void argmax_cand_kernel(const float2 *__restrict__ cand, int nc,
@@ -277,15 +349,22 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
                                                    const float *__restrict__ v_raw, const float *__restrict__ qw,
                                                    const float *__restrict__ kw, int qk_norm, float eps, int n_heads,
                                                    int n_kv, int hd, int S, const StepState *__restrict__ st,
-                                                   float *__restrict__ kc, float *__restrict__ vc,
+                                                   float *__restrict__ kc, float *__restrict__ vc, size_t seq_stride,
                                                    const float2 *__restrict__ rope_cs, float *__restrict__ part) {
     __shared__ __align__(16) float qh[256], kh[256], vh[256];
     __shared__ float red[16], w_m[4], w_l[4];
     __shared__ __align__(16) float w_o[4][256];
-    const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int h = blockIdx.x, s = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int group = n_heads / n_kv, kvh = h / group;
     const int q_dim = n_heads * hd, kv_dim = n_kv * hd, half = hd / 2;
-    const int pos = st->pos;
+    // sequence b: its q/k/v rows, KV cache and partials
+    q_raw += (size_t)b * q_dim;
+    k_raw += (size_t)b * kv_dim;
+    v_raw += (size_t)b * kv_dim;
+    kc += (size_t)b * seq_stride;
+    vc += (size_t)b * seq_stride;
+    part += (size_t)b * n_heads * S * (hd + 2);
+    const int pos = st[b].pos;
     float inv_q = 1.0f, inv_k = 1.0f;
     if (qk_norm) {  // both sums of squares in one pass, one reduction
         float sq = 0.0f, sk = 0.0f;
@@ -412,8 +491,9 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part, int hd, int S,
                                                          float *__restrict__ ao) {
     __shared__ float wa[64], s_inv;
-    const int h = blockIdx.x;
-    const float *ph = part + (size_t)h * S * (hd + 2);
+    const int h = blockIdx.x, b = blockIdx.y, n_heads = gridDim.x;
+    const float *ph = part + ((size_t)b * n_heads + h) * S * (hd + 2);
+    ao += (size_t)b * n_heads * hd;
     if (threadIdx.x < 64) {  // S <= 64 split weights, by wave 0
         const int q = threadIdx.x;
         const float m = q < S ? ph[(size_t)q * (hd + 2)] : -INFINITY;
@@ -452,6 +532,8 @@ __global__ __launch_bounds__(256) void wo_kernel(const float *__restrict__ ao, i
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w, int n,
                                                        float eps, float *__restrict__ out) {
     __shared__ float red[16];
+    x += (size_t)blockIdx.x * n;  // one row per block
+    out += (size_t)blockIdx.x * n;
     const float inv = rms_inv(x, n, eps, red);
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
 }
@@ -464,6 +546,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
                                                       int32_t *__restrict__ seq, int ctx) {
     __shared__ float bv[16];
     __shared__ int bi[16];
+    v += (size_t)blockIdx.x * n;  // one sequence per block
+    st += blockIdx.x;
+    seq += (size_t)blockIdx.x * ctx;
     float best = -INFINITY;
     int idx = n;  // n: nothing found yet
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
@@ -506,9 +591,10 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
     }
 }
 
-// advances the step record without an argmax (prompt positions whose logits nobody reads)
-__global__ void advance_kernel(StepState *st) {
-    if (threadIdx.x == 0) st->pos = st->pos + 1;
+// advances the step records without an argmax (prompt positions whose logits nobody reads)
+__global__ void advance_kernel(StepState *st, int B) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) st[b].pos = st[b].pos + 1;
 }
 
 inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -556,11 +642,52 @@ hipError_t launch_dense_mode(const Launch &L, int dtype, int D, const float *x, 
 }  // namespace
 
 hipError_t launch_embed(const Launch &L, int dtype, const void *emb, int D, int vocab, const StepState *st,
-                        const int32_t *seq, float *x) {
-    const dim3 g((unsigned)((D + 255) / 256)), b(256);
+                        const int32_t *seq, int ctx, float *x, int B) {
+    const dim3 g((unsigned)((D + 255) / 256), (unsigned)B), b(256);
     const uint8_t *e = static_cast<const uint8_t *>(emb);
-    return dtype == RBT_DT_BF16 ? launch(L, embed_kernel<RBT_DT_BF16>, g, b, 0, e, D, vocab, st, seq, x)
-                                : launch(L, embed_kernel<RBT_DT_F32>, g, b, 0, e, D, vocab, st, seq, x);
+    return dtype == RBT_DT_BF16 ? launch(L, embed_kernel<RBT_DT_BF16>, g, b, 0, e, D, vocab, st, seq, ctx, x)
+                                : launch(L, embed_kernel<RBT_DT_F32>, g, b, 0, e, D, vocab, st, seq, ctx, x);
+}
+
+template <int DT, int MODE>
+hipError_t dense_batch_dt(const Launch &L, int D, const float *xin, int B, const Segs &sg, int total, float *resid) {
+    constexpr int step = DT == RBT_DT_BF16 ? 512 : 256;
+    constexpr int RPW = 4;
+    const dim3 g((unsigned)((total + 4 * RPW - 1) / (4 * RPW))), b(256);
+    switch (D / step) {
+#define DB_CASE(nc) \
+    case nc:        \
+        return launch(L, dense_batch_kernel<DT, nc, RPW, MODE>, g, b, 0, xin, B, sg, total, resid);
+        DB_CASE(1)
+        DB_CASE(2)
+        DB_CASE(3)
+        DB_CASE(4)
+        DB_CASE(5)
+        DB_CASE(6)
+        DB_CASE(7)
+        DB_CASE(8)
+#undef DB_CASE
+        default:
+            return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_dense_batch(const Launch &L, int dtype, const float *xin, int B, int D, const void *const W[3],
+                              float *const out[3], const int rows[3], float *resid) {
+    Segs sg;
+    int total = 0;
+    for (int i = 0; i < 3; ++i) {
+        sg.W[i] = static_cast<const uint8_t *>(W[i]);
+        sg.out[i] = out[i];
+        sg.rows[i] = rows[i];
+        total += rows[i];
+    }
+    if (total == 0 || B == 0) return hipSuccess;
+    if (resid)
+        return dtype == RBT_DT_BF16 ? dense_batch_dt<RBT_DT_BF16, 1>(L, D, xin, B, sg, total, resid)
+                                    : dense_batch_dt<RBT_DT_F32, 1>(L, D, xin, B, sg, total, resid);
+    return dtype == RBT_DT_BF16 ? dense_batch_dt<RBT_DT_BF16, 0>(L, D, xin, B, sg, total, nullptr)
+                                : dense_batch_dt<RBT_DT_F32, 0>(L, D, xin, B, sg, total, nullptr);
 }
 
 hipError_t launch_norm_matvec(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
@@ -630,14 +757,15 @@ hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const
 
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
-                            const StepState *st, float *kc, float *vc, const float2 *rope_cs, float *part) {
-    if (hd > kWave * kAttnMaxE) return hipErrorInvalidValue;
-    return launch(L, attn_kernel, dim3((unsigned)n_heads, (unsigned)S), dim3(256), 0, q, k, v, qw, kw, qk_norm, eps,
-                  n_heads, n_kv, hd, S, st, kc, vc, rope_cs, part);
+                            const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
+                            float *part, int B) {
+    if (hd > kWave * kAttnMaxE || S > 64) return hipErrorInvalidValue;
+    return launch(L, attn_kernel, dim3((unsigned)n_heads, (unsigned)S, (unsigned)B), dim3(256), 0, q, k, v, qw, kw,
+                  qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc, seq_stride, rope_cs, part);
 }
 
-hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao) {
-    return launch(L, attn_merge_kernel, dim3((unsigned)n_heads), dim3(256), 0, part, hd, S, ao);
+hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B) {
+    return launch(L, attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)B), dim3(256), 0, part, hd, S, ao);
 }
 
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x) {
@@ -652,16 +780,16 @@ hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, con
                : launch(L, wo_kernel<RBT_DT_F32, false>, g, b, lds, ao, q_dim, W, D, x);
 }
 
-hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out) {
-    return launch(L, rmsnorm_kernel, dim3(1), dim3(1024), 0, x, w, n, eps, out);
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B) {
+    return launch(L, rmsnorm_kernel, dim3((unsigned)B), dim3(1024), 0, x, w, n, eps, out);
 }
 
-hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx) {
-    return launch(L, argmax_kernel, dim3(1), dim3(1024), 0, v, n, st, seq, ctx);
+hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B) {
+    return launch(L, argmax_kernel, dim3((unsigned)B), dim3(1024), 0, v, n, st, seq, ctx);
 }
 
-hipError_t launch_advance(const Launch &L, StepState *st) {
-    return launch(L, advance_kernel, dim3(1), dim3(64), 0, st);
+hipError_t launch_advance(const Launch &L, StepState *st, int B) {
+    return launch(L, advance_kernel, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, st, B);
 }
 
 }  // namespace rbt

@@ -159,8 +159,10 @@ struct StepState {
     int32_t last;      // the last argmax result
     int32_t pad;
 };
+// Per-token kernels take B sequences: sequence b has the record st[b], the token row seq[b * ctx ..),
+// and rows b of x / q / k / v / attn_out / logits.
 hipError_t launch_embed(const Launch &L, int dtype, const void *emb, int D, int vocab, const StepState *st,
-                        const int32_t *seq, float *x);
+                        const int32_t *seq, int ctx, float *x, int B);
 // out_s = W_s (x * inv * nw) for up to three row segments (rows[s] may be 0); W_s rows have D elements.
 hipError_t launch_norm_matvec(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
                               const void *const W[3], float *const out[3], const int rows[3]);
@@ -180,14 +182,20 @@ hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const
 // Attention of one step: grid (n_heads, S splits of the positions), each block writes its partial
 // (m, l, o[hd]) to part [n_heads][S][hd + 2]; launch_attn_merge merges them into ao (S <= 64).
 // rope_cs: [ctx][hd/2] (cos, sin) of the engine's RoPE angles. hd <= 256.
+// kc/vc: this layer's cache of sequence 0; sequence b's starts seq_stride floats further.
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
-                            const StepState *st, float *kc, float *vc, const float2 *rope_cs, float *part);
-hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao);
+                            const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
+                            float *part, int B);
+hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B);
+// Dense rows over B token vectors xin [B][D] (batched decode): out_s [B][rows_s], or with resid != NULL
+// resid [B][rows] += (one segment). Same row shapes as dense_supported.
+hipError_t launch_dense_batch(const Launch &L, int dtype, const float *xin, int B, int D, const void *const W[3],
+                              float *const out[3], const int rows[3], float *resid);
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x);
-hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out);
-hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx);
-hipError_t launch_advance(const Launch &L, StepState *st);
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B);
+hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B);
+hipError_t launch_advance(const Launch &L, StepState *st, int B);
 
 // Dense matvec (one row per wave).
 hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);

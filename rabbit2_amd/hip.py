@@ -21,7 +21,8 @@ EXPORTS = (
     "rbt_hip_matvec", "rbt_hip_matvec_dev", "rbt_hip_malloc", "rbt_hip_free_dev", "rbt_hip_h2d", "rbt_hip_d2h",
     "rbt_hip_memset_dev", "rbt_hip_synchronize", "rbt_hip_stream", "rbt_hip_fill_normal", "rbt_hip_profile_enable",
     "rbt_hip_profile_get", "rbt_hip_set_option", "rbt_hip_state_init", "rbt_hip_forward", "rbt_hip_generate",
-    "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats",
+    "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
+    "rbt_hip_forward_batch", "rbt_hip_generate_batch",
 )
 
 
@@ -83,6 +84,9 @@ def lib():
         L.rbt_hip_tensor.argtypes = [vp, C.c_char_p, i32, C.POINTER(u64), C.POINTER(u64)]
         L.rbt_hip_upload_file.argtypes = [vp, C.c_char_p, C.POINTER(Config)]
         L.rbt_hip_expert_stats.argtypes = [vp, C.POINTER(C.c_uint64)]
+        L.rbt_hip_batch_init.argtypes = [vp, i32, i32]
+        L.rbt_hip_forward_batch.argtypes = [vp, vp, vp, vp, vp]
+        L.rbt_hip_generate_batch.argtypes = [vp, vp, i32, i32, vp, C.POINTER(C.c_double)]
         _lib = L
     return _lib
 
@@ -255,6 +259,28 @@ class Device:
         routing = np.zeros((n_layers, top_k), np.int32)
         self._check(self.L.rbt_hip_forward(self.h, int(token), int(pos), _p(logits), _p(routing)))
         return logits, routing
+
+    def batch_init(self, n_seq, ctx=0):
+        self._check(self.L.rbt_hip_batch_init(self.h, n_seq, ctx))
+
+    def forward_batch(self, tokens, pos, vocab, n_layers, top_k):
+        """One step for every sequence: (logits [B][vocab], routing [n_layers][B][top_k])."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        pos = np.ascontiguousarray(pos, dtype=np.int32)
+        B = tokens.size
+        logits = np.zeros((B, vocab), np.float32)
+        routing = np.zeros((n_layers, B, top_k), np.int32)
+        self._check(self.L.rbt_hip_forward_batch(self.h, _p(tokens), _p(pos), _p(logits), _p(routing)))
+        return logits, routing
+
+    def generate_batch(self, prompts, n_gen):
+        """Greedy --gen of every sequence: (ids [B][n_gen], [prompt ms, generation ms])."""
+        prompts = np.ascontiguousarray(prompts, dtype=np.int32)
+        B, n_prompt = prompts.shape
+        out = np.zeros((B, max(n_gen, 1)), np.int32)
+        ms = (C.c_double * 2)()
+        self._check(self.L.rbt_hip_generate_batch(self.h, _p(prompts), n_prompt, int(n_gen), _p(out), ms))
+        return out[:, :n_gen], (ms[0], ms[1])
 
     def generate(self, prompt, n_gen, eos=-1):
         """Greedy --gen loop on the device: (generated ids, [prompt ms, generation ms])."""

@@ -1,0 +1,113 @@
+"""Batched decode (rbt_hip_batch_init / rbt_hip_forward_batch / rbt_hip_generate_batch): n_seq
+independent sequences stepped together, each with its own KV cache. Each sequence must behave as the
+engine's forward() on that sequence alone (rabbit2/src/rabbit2.c:453-548, the --dump and --gen loops
+:703-740): the oracle (bitwise the reference engine, pinned by the golden fixtures) runs every
+sequence on its own, and the batch must match it -- routing identical in every (token, layer),
+logits normwise within 1e-3, greedy ids identical. Batches of 16+ tokens take the grouped MoE path.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+from tests.common import normwise_err
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = os.path.join(HERE, "golden")
+MANIFEST = json.load(open(os.path.join(GOLDEN, "manifest.json")))
+LOGIT_RTOL = 1e-3
+
+
+def build(case):
+    spec = MANIFEST["cases"][case]
+    cfg = po.Config(**spec["config"])
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    return spec, cfg, model
+
+
+def prompts_for(cfg, B, n, seed):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, cfg.vocab, (B, n)).astype(np.int32)
+
+
+# (case, B, positions): tiny models with the per-token fallbacks and the dense batch kernels, and the
+# OLMoE-shaped layer at 16 sequences (grouped MoE path, batched dense matvecs, 16 heads x 128)
+CASES = [("tiny_olmoe_f32", 3, 6), ("ref_odd_shape", 4, 5), ("ref_qknorm_norenorm", 5, 5),
+         ("olmoe_layer_bf16", 16, 3)]
+
+
+@pytest.mark.parametrize("case,B,n", CASES, ids=[c[0] + f"_B{c[1]}" for c in CASES])
+def test_forward_batch_matches_each_sequence_alone(dev, case, B, n):
+    spec, cfg, model = build(case)
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, n, seed=B)
+    want = [po.run(model, prompts[b], order=po.ORDER_AVX2) for b in range(B)]
+    dev.batch_init(B, 0)
+    for p in range(n):
+        logits, routing = dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
+                                            cfg.top_k)
+        for b in range(B):
+            wl, wr, _ = want[b]
+            assert np.array_equal(routing[:, b, :], wr[p]), f"{case} seq {b} pos {p}"
+            err = normwise_err(logits[b], wl[p])
+            assert err <= LOGIT_RTOL, f"{case} seq {b} pos {p}: logits error {err:.2e}"
+
+
+def test_forward_batch_sequences_restart_independently(dev):
+    """Sequence 1 starts over at position 0 every 3 steps while sequence 0 runs on: each is its own
+    forward() stream (a restart overwrites only that sequence's cache)."""
+    spec, cfg, model = build("tiny_olmoe_bf16")
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, 2, 7, seed=3)
+    dev.batch_init(2, 0)
+    for p in range(7):
+        pos = np.array([p, p % 3], np.int32)
+        logits, routing = dev.forward_batch(prompts[:, p], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
+        w0 = po.run(model, prompts[0, :p + 1], order=po.ORDER_AVX2)
+        s1 = prompts[1, p - p % 3:p + 1]
+        w1 = po.run(model, s1, order=po.ORDER_AVX2)
+        assert np.array_equal(routing[:, 0, :], w0[1][p])
+        assert np.array_equal(routing[:, 1, :], w1[1][len(s1) - 1])
+        assert normwise_err(logits[0], w0[0][p]) <= LOGIT_RTOL
+        assert normwise_err(logits[1], w1[0][len(s1) - 1]) <= LOGIT_RTOL
+
+
+@pytest.mark.parametrize("case,B", [("ref_bf16", 4), ("olmoe_layer_bf16", 16)])
+def test_generate_batch_matches_each_sequence_alone(dev, case, B):
+    spec, cfg, model = build(case)
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    fx = np.load(os.path.join(GOLDEN, case + ".npz"))
+    n = len(fx["tokens"])
+    prompts = prompts_for(cfg, B, n, seed=11)
+    prompts[0] = fx["tokens"]  # sequence 0: the fixture's prompt, whose --gen ids the reference wrote
+    n_gen = spec["n_gen"]
+    dev.batch_init(B, n + n_gen)
+    ids, ms = dev.generate_batch(prompts, n_gen)
+    assert ids[0].tolist() == fx["gen_avx2"].tolist()
+    for b in range(1, B):
+        _, _, gen = po.run(model, prompts[b], order=po.ORDER_AVX2, gen=n_gen, ctx=n + n_gen)
+        assert ids[b].tolist() == gen, f"{case} seq {b}"
+
+
+def test_batch_arguments_checked(dev):
+    from rabbit2_amd.hip import HipError
+    spec, cfg, model = build("ref_bf16")
+    dev.upload(model)
+    dev.batch_init(2, 8)
+    with pytest.raises(HipError):
+        dev.forward(0, 0, cfg.vocab, cfg.n_layers, cfg.top_k)  # the state holds two sequences
+    with pytest.raises(HipError):
+        dev.forward_batch([0, cfg.vocab], [0, 0], cfg.vocab, cfg.n_layers, cfg.top_k)
+    with pytest.raises(HipError):
+        dev.forward_batch([0, 0], [0, 8], cfg.vocab, cfg.n_layers, cfg.top_k)
+    with pytest.raises(HipError):
+        dev.generate_batch(np.zeros((2, 6), np.int32), 3)  # 6 + 3 > ctx 8
