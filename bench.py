@@ -16,7 +16,8 @@ Prints one JSON line: tok/s of the 16-layer MoE stack; the roofline of the domin
 512-token prefill of layer 0 ("prefill": uniform and skewed routing, tokens-per-expert histogram,
 HBM rate and matrix-core utilisation of the grouped GEMMs); the whole OLMoE-1B-7B-shaped model
 ("full_model": 16 layers with attention, vocab 50304, a 128-token prompt and 256 greedy tokens
-through the device-side generate loop); and the CPU baselines (the oracle, the engine's own
+through the device-side generate loop, and "batched_decode": 32 sequences with 2048-token contexts, 64
+greedy tokens each); and the CPU baselines (the oracle, the engine's own
 arithmetic in its AVX2 order, on one host core).
 """
 import argparse
@@ -95,6 +96,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill leg")
     ap.add_argument("--prefill-reps", type=int, default=20, help="timed calls per prefill workload")
     ap.add_argument("--no-full-model", action="store_true", help="skip the whole-model generate leg")
+    ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode leg")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one device-to-device copy of this size (a known-size kernel for scaling "
                          "FETCH_SIZE/WRITE_SIZE counters)")
@@ -296,7 +298,7 @@ def main():
         out["cpu_baseline"] = cpu_baseline(dev, routers, experts, stride, xs_host, args.cpu_seconds)
 
     if not args.no_full_model:
-        out["full_model"] = full_model_leg(not args.no_cpu, args.cpu_seconds)
+        out["full_model"] = full_model_leg(not args.no_cpu, args.cpu_seconds, not args.no_batched)
 
     print(json.dumps(out), flush=True)
     dev.close()
@@ -312,7 +314,7 @@ FULL_MATS = ("wq", "wk", "wv", "wo", "router", "experts")
 FULL_NORMS = ("attn_norm", "q_norm", "k_norm", "ffn_norm")
 
 
-def full_model_leg(with_cpu, cpu_seconds):
+def full_model_leg(with_cpu, cpu_seconds, batched=True):
     """128 random prompt ids, then 256 greedy tokens through rbt_hip_generate (one HIP graph replay
     per token, the argmax feeding the next step on the device). Reports generated tok/s, prompt tok/s
     and the weight bytes streamed per generated token."""
@@ -372,8 +374,45 @@ def full_model_leg(with_cpu, cpu_seconds):
     }
     if with_cpu:
         res["cpu_baseline"] = cpu_full_model(dev, cfg, prompt, cpu_seconds)
+    if batched:
+        res["batched_decode"] = batched_leg(dev, cfg)
     dev.close()
     return res
+
+
+B_SEQ, B_CTX, B_GEN = 32, 2048, 64
+
+
+def batched_leg(dev, cfg):
+    """32 independent sequences on the same model, each with a 2048-token random-id context run through
+    the model into its own KV cache (the prompt phase of rbt_hip_generate_batch), then 64 greedy tokens
+    each, all sequences in one step (every expert is touched every step)."""
+    dev.batch_init(B_SEQ, B_CTX + B_GEN)
+    prompts = np.random.default_rng(SEED + 5).integers(0, cfg.vocab, (B_SEQ, B_CTX)).astype(np.int32)
+    ids, (p_ms, g_ms) = dev.generate_batch(prompts, B_GEN)
+    assert ids.shape == (B_SEQ, B_GEN) and ids.min() >= 0 and ids.max() < cfg.vocab
+    steps = B_GEN - 1
+    D_, hd = cfg.dim, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    esz = 2
+    dense = cfg.n_layers * ((qd + 2 * kvd) * D_ + D_ * qd + cfg.n_experts * D_) * esz + cfg.vocab * D_ * esz
+    experts = cfg.n_layers * cfg.n_experts * 3 * cfg.expert_hidden * D_ * esz  # every expert, every step
+    mean_pos = B_CTX + B_GEN / 2.0
+    kv = B_SEQ * cfg.n_layers * 2 * kvd * 4 * mean_pos
+    step_bytes = dense + experts + kv
+    ms_step = g_ms / steps
+    return {
+        "workload": f"{B_SEQ} sequences x {B_CTX}-token random-id context in the KV cache, {B_GEN} greedy tokens "
+                    "each, one step for all sequences (OLMoE-1B-7B shape, f32 KV cache)",
+        "tok_per_s": round(B_SEQ * steps / (g_ms * 1e-3), 1),
+        "ms_per_step": round(ms_step, 3),
+        "context_fill_s": round(p_ms * 1e-3, 2),
+        "bytes_per_step": int(step_bytes),
+        "hbm_GBps_alg": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "hbm_frac_alg": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "note": "bytes per step: dense weights once, all 64 experts of every layer, the 32 KV caches at the mean "
+                "position",
+    }
 
 
 def cpu_full_model(dev, cfg, prompt, seconds):
