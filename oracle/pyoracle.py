@@ -86,6 +86,11 @@ def lib():
         L.orc_topk.argtypes = [vp, i32, i32, vp, vp, vp, vp]
         L.orc_moe_layer.argtypes = [C.POINTER(MoeDesc), vp, i32, i32, vp, vp, vp, vp, vp]
         L.orc_run.argtypes = [vp, u64, vp, i32, i32, i32, vp, vp, i32, C.c_int32, vp, C.POINTER(C.c_int)]
+        L.orc_run_sampled.argtypes = [vp, u64, vp, i32, i32, i32, vp, vp, i32, C.c_int32, vp, C.POINTER(C.c_int),
+                                      C.c_float, i32, C.c_float, u64]
+        L.orc_rng_next.argtypes, L.orc_rng_next.restype = [C.POINTER(C.c_uint64)], u64
+        L.orc_rng_uniform.argtypes, L.orc_rng_uniform.restype = [C.POINTER(C.c_uint64)], C.c_double
+        L.orc_sample.argtypes = [vp, i32, C.c_float, i32, C.c_float, C.POINTER(C.c_uint64), vp, vp]
         L.orc_last_error.restype = C.c_char_p
         L.orc_parse_header.argtypes = [vp, u64, C.POINTER(Config)]
         L.orc_splitmix64_next.argtypes, L.orc_splitmix64_next.restype = [C.POINTER(C.c_uint64)], u64
@@ -178,8 +183,9 @@ def parse_header(buf):
     return cfg
 
 
-def run(model, tokens, order=ORDER_SCALAR, ctx=0, gen=0, eos=-1):
-    """The --dump/--gen behaviour of the engine. model: uint8 array of the .rbt2 bytes."""
+def run(model, tokens, order=ORDER_SCALAR, ctx=0, gen=0, eos=-1, temperature=0.0, top_k=0, top_p=1.0, seed=0):
+    """The --dump/--gen behaviour of the engine. model: uint8 array of the .rbt2 bytes. temperature > 0
+    samples the generated tokens like --temperature/--top-k/--top-p/--seed."""
     cfg = parse_header(model)
     tok = np.ascontiguousarray(tokens, dtype=np.int32)
     nt = tok.size
@@ -187,10 +193,26 @@ def run(model, tokens, order=ORDER_SCALAR, ctx=0, gen=0, eos=-1):
     routing = np.zeros((nt, cfg.n_layers, cfg.top_k), np.int32)
     gen_out = np.zeros(max(gen, 1), np.int32)
     ng = C.c_int(0)
-    if not lib().orc_run(_p(model), model.size, _p(tok), nt, ctx, order, _p(logits), _p(routing), gen, eos,
-                         _p(gen_out), C.byref(ng)):
+    if not lib().orc_run_sampled(_p(model), model.size, _p(tok), nt, ctx, order, _p(logits), _p(routing), gen, eos,
+                         _p(gen_out), C.byref(ng), temperature, top_k, top_p, seed):
         raise RuntimeError(lib().orc_last_error().decode())
     return logits, routing, gen_out[:ng.value].tolist()
+
+
+def sample(logits, temperature, top_k, top_p, rng_state):
+    """sample_logits on one logits row; returns (token, new rng state)."""
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    st = C.c_uint64(rng_state)
+    idx = np.zeros(v.size, np.int32)
+    prob = np.zeros(v.size, np.float32)
+    t = lib().orc_sample(_p(v), v.size, temperature, top_k, top_p, C.byref(st), _p(idx), _p(prob))
+    return t, st.value
+
+
+def rng_next(state):
+    st = C.c_uint64(state)
+    v = lib().orc_rng_next(C.byref(st))
+    return v, st.value
 
 
 def splitmix64(state, n):

@@ -438,6 +438,86 @@ static int argmax(const float *v, int n) {
     return best;
 }
 
+/* ---- sampling, rabbit2.c:558-610: xorshift64* state (a zero state counts as the golden-ratio
+ * constant), uniform doubles from its top 53 bits, and sample_logits: temperature, top-k by K rounds
+ * of "largest remaining, first index on ties" swapped to the front, softmax over the kept values
+ * (max-subtract, expf, sequential sum, divide), top-p over the kept order, then the first position
+ * whose running double sum exceeds the draw. */
+uint64_t orc_rng_next(uint64_t *s) {
+    uint64_t x = *s ? *s : 0x9E3779B97F4A7C15ULL;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *s = x;
+    return x * 2685821657736338717ULL;
+}
+
+double orc_rng_uniform(uint64_t *s) { return (double)(orc_rng_next(s) >> 11) * (1.0 / 9007199254740992.0); }
+
+int orc_sample(const float *logits, int n, float temperature, int top_k, float top_p, uint64_t *rng, int32_t *idx,
+               float *prob) {
+    if (temperature <= 0.0f) return argmax(logits, n);
+    for (int i = 0; i < n; i++) {
+        idx[i] = i;
+        prob[i] = logits[i] / temperature;
+    }
+    const int use_k = top_k > 0 && top_k < n;
+    if (use_k) {
+        for (int i = 0; i < top_k; i++) {
+            int best = i;
+            for (int j = i + 1; j < n; j++)
+                if (prob[j] > prob[best]) best = j;
+            const float tp = prob[i];
+            prob[i] = prob[best];
+            prob[best] = tp;
+            const int32_t ti = idx[i];
+            idx[i] = idx[best];
+            idx[best] = ti;
+        }
+        for (int i = top_k; i < n; i++) prob[i] = -INFINITY;
+    }
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++)
+        if (prob[i] > mx) mx = prob[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        if (isfinite(prob[i])) {
+            prob[i] = expf(prob[i] - mx);
+            sum += prob[i];
+        } else {
+            prob[i] = 0.0f;
+        }
+    }
+    if (!(sum > 0.0f)) return argmax(logits, n);
+    for (int i = 0; i < n; i++) prob[i] /= sum;
+    if (top_p > 0.0f && top_p < 1.0f) {
+        const int m = use_k ? top_k : n;
+        float cum = 0.0f;
+        int keep = m;
+        for (int i = 0; i < m; i++) {
+            cum += prob[i];
+            if (cum >= top_p) {
+                keep = i + 1;
+                break;
+            }
+        }
+        for (int i = keep; i < n; i++) prob[i] = 0.0f;
+        sum = 0.0f;
+        for (int i = 0; i < n; i++) sum += prob[i];
+        if (!(sum > 0.0f)) return idx[0];
+        for (int i = 0; i < n; i++) prob[i] /= sum;
+    }
+    const double r = orc_rng_uniform(rng);
+    double cum = 0.0;
+    for (int i = 0; i < n; i++) {
+        cum += prob[i];
+        if (r < cum) return idx[i];
+    }
+    for (int i = n - 1; i >= 0; i--)
+        if (prob[i] > 0.0f) return idx[i];
+    return argmax(logits, n);
+}
+
 static void engine_free(engine *g) {
     free(g->ly);
     free(g->x);
@@ -455,6 +535,13 @@ static void engine_free(engine *g) {
 
 int orc_run(const unsigned char *file, uint64_t file_size, const int32_t *tokens, int nt, int ctx, int order,
             float *logits, int32_t *routing, int gen, int32_t eos, int32_t *gen_out, int *n_gen) {
+    return orc_run_sampled(file, file_size, tokens, nt, ctx, order, logits, routing, gen, eos, gen_out, n_gen, 0.0f, 0,
+                           1.0f, 0);
+}
+
+int orc_run_sampled(const unsigned char *file, uint64_t file_size, const int32_t *tokens, int nt, int ctx, int order,
+                    float *logits, int32_t *routing, int gen, int32_t eos, int32_t *gen_out, int *n_gen,
+                    float temperature, int top_k, float top_p, uint64_t seed) {
     engine g;
     memset(&g, 0, sizeof g);
     if (n_gen) *n_gen = 0;
@@ -511,8 +598,18 @@ int orc_run(const unsigned char *file, uint64_t file_size, const int32_t *tokens
     if (gen > 0) {
         if (gen > ctx - nt) gen = ctx - nt;
         int pos = nt, produced = 0;
+        uint64_t rng = seed ? seed : 0x9E3779B97F4A7C15ULL; /* rabbit2.c:723 */
+        int32_t *sidx = (int32_t *)malloc(sizeof(int32_t) * (size_t)c->vocab);
+        float *sprob = (float *)malloc(sizeof(float) * (size_t)c->vocab);
+        if (!sidx || !sprob) {
+            free(sidx);
+            free(sprob);
+            free(rt);
+            engine_free(&g);
+            return fail("out of memory");
+        }
         for (int j = 0; j < gen; j++) {
-            int next = argmax(g.logits, c->vocab);
+            int next = orc_sample(g.logits, c->vocab, temperature, top_k, top_p, &rng, sidx, sprob);
             if (gen_out) gen_out[produced] = next;
             produced++;
             if (next == eos) break;
@@ -520,6 +617,8 @@ int orc_run(const unsigned char *file, uint64_t file_size, const int32_t *tokens
             forward(&g, next, pos++, rt, order);
         }
         if (n_gen) *n_gen = produced;
+        free(sidx);
+        free(sprob);
     }
     free(rt);
     engine_free(&g);

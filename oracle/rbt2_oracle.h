@@ -96,6 +96,16 @@ int orc_moe_layer(const orc_moe_desc *d, const float *xb, int T, int order, floa
  * Returns 1 on success, 0 on a malformed model / bad arguments (message in orc_last_error()). */
 int orc_run(const unsigned char *file, uint64_t file_size, const int32_t *tokens, int nt, int ctx, int order,
             float *logits, int32_t *routing, int gen, int32_t eos, int32_t *gen_out, int *n_gen);
+/* The same with the engine's sampling for the generated tokens (--temperature, --top-k, --top-p,
+ * --seed; rabbit2.c:558-610, :634-638, :716-740); temperature <= 0 is greedy. */
+int orc_run_sampled(const unsigned char *file, uint64_t file_size, const int32_t *tokens, int nt, int ctx, int order,
+                    float *logits, int32_t *routing, int gen, int32_t eos, int32_t *gen_out, int *n_gen,
+                    float temperature, int top_k, float top_p, uint64_t seed);
+/* sample_logits (rabbit2.c:569-610) and its generator (:558-567); idx/prob: [n] scratch. */
+uint64_t orc_rng_next(uint64_t *state);
+double orc_rng_uniform(uint64_t *state);
+int orc_sample(const float *logits, int n, float temperature, int top_k, float top_p, uint64_t *rng, int32_t *idx,
+               float *prob);
 const char *orc_last_error(void);
 
 /* Parse + validate a header (rabbit2.c:199-228). Returns 1 and fills *c on success. */
