@@ -156,6 +156,14 @@ int rbt_hip_forward_batch(rbt_hip *h, const int32_t *tokens, const int32_t *pos,
  * all sequences. ms_out (may be NULL): [prompt ms, generation ms]. */
 int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int n_gen, int32_t *out, double *ms_out);
 
+/* How rbt_hip_generate / rbt_hip_generate_batch pick tokens: the engine's --temperature, --top-k,
+ * --top-p and --seed (rabbit2.c:569-610, :634-638, :723). temperature <= 0 (the default) is greedy;
+ * otherwise each generated token is drawn on the device exactly as sample_logits does, with the
+ * xorshift64* generator seeded by seed (0 = the engine's default constant), every sequence of a batch
+ * from the same seed. The draws equal the engine's wherever its logits do (the device logits agree with
+ * the engine's to rounding). */
+int rbt_hip_set_sampling(rbt_hip *h, float temperature, int top_k, float top_p, uint64_t seed);
+
 /* A model image built in place on the device instead of uploaded (no counterpart in the reference,
  * whose synthetic models are written to files by rabbit2/ref/rbt2.py): validates cfg like
  * rbt_hip_upload, allocates the image with the file layout (rabbit2.c:158-193) and returns its device

@@ -60,6 +60,8 @@ struct DecodeState {
     float *part = nullptr;        // attention split partials [n_heads][S][hd + 2]
     float2 *rope_cs = nullptr;    // [ctx][hd/2] (cos, sin) of the RoPE angles
     float2 *cand = nullptr;       // lm_head blocks' argmax candidates
+    float *sprob = nullptr;       // sampler scratch [n_seq][vocab]
+    int32_t *sidx = nullptr;      // sampler scratch [n_seq][vocab]
     float *logits = nullptr;      // [vocab]
     int32_t *routing = nullptr;   // [n_layers][n_seq][top_k]
     int32_t *seq = nullptr;       // [n_seq][ctx] token of each position
@@ -93,6 +95,8 @@ struct rbt_hip {
     DecodeState ds;
     Profile prof;
     int fused_decode = 1;  // option "fused_decode": batch-1 top-k inside the gate/up kernel
+    Sampling sampling;     // rbt_hip_set_sampling: how rbt_hip_generate* pick tokens
+    uint64_t seed = 0;
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
     const int32_t *expert_counts = nullptr;  // histogram of the last grouped-path call
     // staging for the host-pointer entry points
@@ -376,11 +380,14 @@ int enqueue_step(rbt_hip *h, bool final) {
         const int rows[3] = {c.vocab, 0, 0};
         const float *fn = reinterpret_cast<const float *>(h->model + h->final_norm);
         const bool dense = dense_supported(c.dtype, D, W, rows);
-        if (B == 1 && dense) {  // lm_head with per-block argmax candidates, then the argmax
+        const bool sample = h->sampling.temperature > 0.0f;
+        if (B == 1 && dense && !sample) {  // lm_head with per-block argmax candidates, then the argmax
             STEP_LAUNCH(kProfLmHead, launch_dense_argmax(L, c.dtype, ds.x, fn, c.rms_eps, D, W[0], c.vocab, ds.logits,
                                                          ds.cand, ds.st, ds.seq, ds.ctx));
         } else {
-            if (dense) {
+            if (dense && B == 1) {
+                STEP_LAUNCH(kProfLmHead, launch_dense_norm(L, c.dtype, ds.x, fn, c.rms_eps, D, W, out, rows));
+            } else if (dense) {
                 STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B));
                 STEP_LAUNCH(kProfLmHead, launch_dense_batch(L, c.dtype, ds.xb, B, D, W, out, rows, nullptr));
             } else {
@@ -390,7 +397,11 @@ int enqueue_step(rbt_hip *h, bool final) {
                                                                 ob, rows));
                 }
             }
-            STEP_LAUNCH(kProfArgmax, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx, B));
+            if (sample)
+                STEP_LAUNCH(kProfArgmax, launch_sample(L, ds.logits, c.vocab, h->sampling, ds.sprob, ds.sidx, ds.st,
+                                                       ds.seq, ds.ctx, B));
+            else
+                STEP_LAUNCH(kProfArgmax, launch_argmax(L, ds.logits, c.vocab, ds.st, ds.seq, ds.ctx, B));
         }
     } else {
         STEP_LAUNCH(-1, launch_advance(L, ds.st, B));
@@ -802,6 +813,16 @@ int rbt_hip_synchronize(rbt_hip *h) {
     return 1;
 }
 
+int rbt_hip_set_sampling(rbt_hip *h, float temperature, int top_k, float top_p, uint64_t seed) {
+    if (!h) return fail(nullptr, "set_sampling: handle is NULL");
+    if (temperature != temperature || top_p != top_p) return fail(h, "set_sampling: NaN argument");
+    h->sampling.temperature = temperature;
+    h->sampling.top_k = top_k;
+    h->sampling.top_p = top_p;
+    h->seed = seed;
+    return 1;
+}
+
 int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
     if (!h || !name) return fail(h, "set_option: NULL argument");
     if (strcmp(name, "fused_decode") == 0) {
@@ -891,6 +912,7 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     const uint64_t o_part = carve(4 * B * c.n_heads * ds.S * (hd + 2));
     const uint64_t o_rope = carve(8 * (uint64_t)ctx * (hd / 2));
     const uint64_t o_cand = carve(8 * (uint64_t)dense_argmax_blocks(c.vocab));
+    const uint64_t o_sp = carve(4 * B * c.vocab), o_si = carve(4 * B * c.vocab);
     const uint64_t o_lg = carve(4 * B * c.vocab), o_rt = carve(4 * B * c.n_layers * c.top_k);
     const uint64_t o_seq = carve(4 * B * ctx), o_st = carve(sizeof(StepState) * B);
     if (c.head_dim > 256 || 4 * D > 64 * 1024 || 4 * qd > 64 * 1024)
@@ -908,6 +930,8 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     ds.part = reinterpret_cast<float *>(b + o_part);
     ds.rope_cs = reinterpret_cast<float2 *>(b + o_rope);
     ds.cand = reinterpret_cast<float2 *>(b + o_cand);
+    ds.sprob = reinterpret_cast<float *>(b + o_sp);
+    ds.sidx = reinterpret_cast<int32_t *>(b + o_si);
     ds.logits = reinterpret_cast<float *>(b + o_lg);
     ds.routing = reinterpret_cast<int32_t *>(b + o_rt);
     ds.seq = reinterpret_cast<int32_t *>(b + o_seq);
@@ -945,10 +969,14 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
     if (token < 0 || token >= c.vocab) return fail(h, "token %d out of range", token);
     if (pos < 0 || pos >= h->ds.ctx) return fail(h, "forward: position %d outside the context of %d", pos, h->ds.ctx);
     if (!set_device(h)) return 0;
-    const StepState st{pos, 0x7FFFFFFF, 0, 0};
+    const StepState st{pos, 0x7FFFFFFF, 0, 0, 0, 0};
     HIP_OK(h, hipMemcpyAsync(h->ds.seq + pos, &token, 4, hipMemcpyHostToDevice, h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
-    if (!enqueue_step(h, true)) return 0;
+    const Sampling sp = h->sampling;
+    h->sampling = Sampling{};  // a forward returns logits; its tail is the (cheap) greedy argmax
+    const int ok = enqueue_step(h, true);
+    h->sampling = sp;
+    if (!ok) return 0;
     if (logits) HIP_OK(h, hipMemcpyAsync(logits, h->ds.logits, 4 * (size_t)c.vocab, hipMemcpyDeviceToHost, h->stream));
     if (routing_out)
         HIP_OK(h, hipMemcpyAsync(routing_out, h->ds.routing, 4 * (size_t)c.n_layers * c.top_k, hipMemcpyDeviceToHost,
@@ -975,7 +1003,7 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
     if (n_gen > ctx - n_prompt) n_gen = ctx - n_prompt;  // rabbit2.c:717
     if (n_gen > 0 && !out) return fail(h, "generate: out is NULL");
     if (!set_device(h)) return 0;
-    const StepState st{0, n_prompt, 0, 0};
+    const StepState st{0, n_prompt, 0, 0, h->seed ? h->seed : 0x9E3779B97F4A7C15ull, 0};  // rabbit2.c:723
     HIP_OK(h, hipMemcpyAsync(h->ds.seq, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
     const bool prof = h->prof.on;
@@ -1037,14 +1065,18 @@ int rbt_hip_forward_batch(rbt_hip *h, const int32_t *tokens, const int32_t *pos,
         if (tokens[b] < 0 || tokens[b] >= c.vocab) return fail(h, "token %d out of range", tokens[b]);
         if (pos[b] < 0 || pos[b] >= h->ds.ctx)
             return fail(h, "forward_batch: position %d outside the context of %d", pos[b], h->ds.ctx);
-        st[(size_t)b] = StepState{pos[b], 0x7FFFFFFF, 0, 0};
+        st[(size_t)b] = StepState{pos[b], 0x7FFFFFFF, 0, 0, 0, 0};
     }
     if (!set_device(h)) return 0;
     for (int b = 0; b < B; b++)
         HIP_OK(h, hipMemcpyAsync(h->ds.seq + (size_t)b * h->ds.ctx + pos[b], tokens + b, 4, hipMemcpyHostToDevice,
                                  h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, st.data(), sizeof(StepState) * B, hipMemcpyHostToDevice, h->stream));
-    if (!enqueue_step(h, true)) return 0;
+    const Sampling sp = h->sampling;
+    h->sampling = Sampling{};
+    const int ok = enqueue_step(h, true);
+    h->sampling = sp;
+    if (!ok) return 0;
     if (logits)
         HIP_OK(h, hipMemcpyAsync(logits, h->ds.logits, 4 * (size_t)B * c.vocab, hipMemcpyDeviceToHost, h->stream));
     if (routing_out)
@@ -1068,7 +1100,7 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
         return fail(h, "generate_batch: n_gen %d outside [0, ctx - n_prompt = %d]", n_gen, ctx - n_prompt);
     if (n_gen > 0 && !out) return fail(h, "generate_batch: out is NULL");
     if (!set_device(h)) return 0;
-    std::vector<StepState> st((size_t)B, StepState{0, n_prompt, 0, 0});
+    std::vector<StepState> st((size_t)B, StepState{0, n_prompt, 0, 0, h->seed ? h->seed : 0x9E3779B97F4A7C15ull, 0});
     for (int b = 0; b < B; b++)
         HIP_OK(h, hipMemcpyAsync(h->ds.seq + (size_t)b * ctx, prompts + (size_t)b * n_prompt, 4 * (size_t)n_prompt,
                                  hipMemcpyHostToDevice, h->stream));

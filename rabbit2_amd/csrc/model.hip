@@ -591,6 +591,161 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
     }
 }
 
+// ---------------------------------------------------------------- sampler (rabbit2.c:558-610)
+// sample_logits for one sequence per block, in the engine's operations and orders: prob = logits / T
+// (idx = i); with 0 < top_k < n, K rounds that each swap the largest remaining value (first position on
+// ties, in the current order) to the front; max, expf(v - max) over the finite values summed in index
+// order, divide; top-p over the first m (K, or n) entries in that order; then the first position whose
+// running double sum passes the xorshift64* draw. The K rounds and elementwise steps run across the
+// block; every sum, whose order fixes its rounding, runs in one thread like the engine's loops.
+__device__ __forceinline__ uint64_t rng_next_dev(uint64_t *s) {
+    uint64_t x = *s ? *s : 0x9E3779B97F4A7C15ull;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *s = x;
+    return x * 2685821657736338717ull;
+}
+
+// first position of the largest value among prob[from..n) (a NaN never wins; -1 if all NaN)
+__device__ __forceinline__ int block_first_max(const float *prob, int from, int n, float *s_b, int *s_i) {
+    float b = 0.0f;
+    int k = -1;
+    for (int i = from + threadIdx.x; i < n; i += blockDim.x) {
+        const float v = prob[i];
+        if (v == v && (k < 0 || v > b)) {
+            b = v;
+            k = i;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_down(b, off, 64);
+        const int ok = __shfl_down(k, off, 64);
+        if (ok >= 0 && (k < 0 || ob > b || (ob == b && ok < k))) {
+            b = ob;
+            k = ok;
+        }
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __syncthreads();  // s_b / s_i are free
+    if (lane == 0) {
+        s_b[wv] = b;
+        s_i[wv] = k;
+    }
+    __syncthreads();
+    b = 0.0f;
+    k = -1;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w)
+        if (s_i[w] >= 0 && (k < 0 || s_b[w] > b || (s_b[w] == b && s_i[w] < k))) {
+            b = s_b[w];
+            k = s_i[w];
+        }
+    return k;
+}
+
+__global__ __launch_bounds__(1024) void sample_kernel(const float *__restrict__ logits, int n, Sampling sp,
+                                                      float *__restrict__ prob, int32_t *__restrict__ idx,
+                                                      StepState *st, int32_t *__restrict__ seq, int ctx) {
+    __shared__ float s_b[16];
+    __shared__ int s_i[16];
+    __shared__ int s_res;
+    const int b = blockIdx.x;
+    logits += (size_t)b * n;
+    prob += (size_t)b * n;
+    idx += (size_t)b * n;
+    st += b;
+    seq += (size_t)b * ctx;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < n; i += blockDim.x) {
+        idx[i] = i;
+        prob[i] = logits[i] / sp.temperature;
+    }
+    const bool use_k = sp.top_k > 0 && sp.top_k < n;
+    if (use_k) {
+        for (int r = 0; r < sp.top_k; ++r) {
+            __syncthreads();  // the previous swap (and the fill) are visible
+            int best = block_first_max(prob, r, n, s_b, s_i);
+            const float pr = prob[r];
+            // the engine's scan starts from position r: a NaN there is never beaten, and nothing beats it
+            // when every value is NaN
+            if (best < 0 || pr != pr) best = r;
+            if (tid == 0 && best != r) {
+                const float tp = prob[r];
+                prob[r] = prob[best];
+                prob[best] = tp;
+                const int32_t ti = idx[r];
+                idx[r] = idx[best];
+                idx[best] = ti;
+            }
+        }
+    }
+    __syncthreads();
+    const int m = use_k ? sp.top_k : n;  // positions past m are -inf under top-k
+    if (tid == 0) {
+        int res = -1;
+        float mx = -INFINITY;
+        for (int i = 0; i < m; ++i)
+            if (prob[i] > mx) mx = prob[i];
+        float sum = 0.0f;
+        for (int i = 0; i < m; ++i) {
+            const float v = prob[i];
+            const float e = isfinite(v) ? expf(v - mx) : 0.0f;
+            prob[i] = e;
+            sum += e;
+        }
+        if (!(sum > 0.0f)) {
+            res = -2;  // the engine falls back to argmax(logits)
+        } else {
+            for (int i = 0; i < m; ++i) prob[i] /= sum;
+            int keep = m;
+            if (sp.top_p > 0.0f && sp.top_p < 1.0f) {
+                float cum = 0.0f;
+                for (int i = 0; i < m; ++i) {
+                    cum += prob[i];
+                    if (cum >= sp.top_p) {
+                        keep = i + 1;
+                        break;
+                    }
+                }
+                float s2 = 0.0f;
+                for (int i = 0; i < keep; ++i) s2 += prob[i];  // zeros past keep add nothing
+                if (!(s2 > 0.0f)) {
+                    res = idx[0];
+                } else {
+                    for (int i = 0; i < keep; ++i) prob[i] /= s2;
+                }
+            }
+            if (res == -1) {
+                uint64_t rng = st->rng;
+                const double r = (double)(rng_next_dev(&rng) >> 11) * (1.0 / 9007199254740992.0);
+                st->rng = rng;
+                double cum = 0.0;
+                for (int i = 0; i < keep && res < 0; ++i) {
+                    cum += prob[i];
+                    if (r < cum) res = idx[i];
+                }
+                for (int i = keep - 1; i >= 0 && res < 0; --i)
+                    if (prob[i] > 0.0f) res = idx[i];
+                if (res < 0) res = -2;
+            }
+        }
+        s_res = res;
+    }
+    __syncthreads();
+    int tok = s_res;
+    if (tok == -2) {  // argmax(logits): first index of the largest, a NaN at 0 kept (rabbit2.c:552-556)
+        tok = block_first_max(logits, 0, n, s_b, s_i);
+        const float v0 = logits[0];
+        if (tok < 0 || v0 != v0) tok = 0;
+    }
+    if (tid == 0) {
+        const int p = st->pos;
+        st->last = tok;
+        if (p + 1 < ctx && p + 1 >= st->n_prompt) seq[p + 1] = tok;
+        st->pos = p + 1;
+    }
+}
+
 // advances the step records without an argmax (prompt positions whose logits nobody reads)
 __global__ void advance_kernel(StepState *st, int B) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -786,6 +941,11 @@ hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n
 
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B) {
     return launch(L, argmax_kernel, dim3((unsigned)B), dim3(1024), 0, v, n, st, seq, ctx);
+}
+
+hipError_t launch_sample(const Launch &L, const float *logits, int n, const Sampling &sp, float *prob, int32_t *idx,
+                         StepState *st, int32_t *seq, int ctx, int B) {
+    return launch(L, sample_kernel, dim3((unsigned)B), dim3(1024), 0, logits, n, sp, prob, idx, st, seq, ctx);
 }
 
 hipError_t launch_advance(const Launch &L, StepState *st, int B) {

@@ -155,10 +155,22 @@ hipError_t launch_router_prefill(const Launch &L, int dtype, const float *xb, co
 // The step record every forward kernel reads: the position being processed; seq[pos] is its token.
 struct StepState {
     int32_t pos;       // position of the step being processed
-    int32_t n_prompt;  // prompt length: the argmax appends tokens to seq[] only past it
-    int32_t last;      // the last argmax result
+    int32_t n_prompt;  // prompt length: the argmax / sampler appends tokens to seq[] only past it
+    int32_t last;      // the last argmax / sampler result
     int32_t pad;
+    uint64_t rng;      // the sampler's xorshift64* state (rabbit2.c:558-567, :723)
+    uint64_t pad2;
 };
+// The engine's sampling settings (--temperature, --top-k, --top-p; rabbit2.c:634-638).
+struct Sampling {
+    float temperature = 0.0f;  // <= 0: greedy
+    int top_k = 0;
+    float top_p = 1.0f;
+};
+// sample_logits (rabbit2.c:569-610) for B sequences, one block each: logits [B][n], scratch prob/idx
+// [B][n]; then the step advances like the argmax.
+hipError_t launch_sample(const Launch &L, const float *logits, int n, const Sampling &sp, float *prob, int32_t *idx,
+                         StepState *st, int32_t *seq, int ctx, int B);
 // Per-token kernels take B sequences: sequence b has the record st[b], the token row seq[b * ctx ..),
 // and rows b of x / q / k / v / attn_out / logits.
 hipError_t launch_embed(const Launch &L, int dtype, const void *emb, int D, int vocab, const StepState *st,

@@ -22,7 +22,7 @@ EXPORTS = (
     "rbt_hip_memset_dev", "rbt_hip_synchronize", "rbt_hip_stream", "rbt_hip_fill_normal", "rbt_hip_profile_enable",
     "rbt_hip_profile_get", "rbt_hip_set_option", "rbt_hip_state_init", "rbt_hip_forward", "rbt_hip_generate",
     "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
-    "rbt_hip_forward_batch", "rbt_hip_generate_batch",
+    "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling",
 )
 
 
@@ -85,6 +85,7 @@ def lib():
         L.rbt_hip_upload_file.argtypes = [vp, C.c_char_p, C.POINTER(Config)]
         L.rbt_hip_expert_stats.argtypes = [vp, C.POINTER(C.c_uint64)]
         L.rbt_hip_batch_init.argtypes = [vp, i32, i32]
+        L.rbt_hip_set_sampling.argtypes = [vp, f32, i32, f32, u64]
         L.rbt_hip_forward_batch.argtypes = [vp, vp, vp, vp, vp]
         L.rbt_hip_generate_batch.argtypes = [vp, vp, i32, i32, vp, C.POINTER(C.c_double)]
         _lib = L
@@ -259,6 +260,9 @@ class Device:
         routing = np.zeros((n_layers, top_k), np.int32)
         self._check(self.L.rbt_hip_forward(self.h, int(token), int(pos), _p(logits), _p(routing)))
         return logits, routing
+
+    def set_sampling(self, temperature=0.0, top_k=0, top_p=1.0, seed=0):
+        self._check(self.L.rbt_hip_set_sampling(self.h, temperature, top_k, top_p, seed))
 
     def batch_init(self, n_seq, ctx=0):
         self._check(self.L.rbt_hip_batch_init(self.h, n_seq, ctx))
