@@ -208,7 +208,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     constexpr int NTILE = kGWRows / MATS;  // output columns per tile
     __shared__ __align__(1024) uint8_t ring[kGStages * kGStageBytes];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, rg = w % kGRG, ch = w / kGRG;
+    // w in a scalar register: the branches on it below are then wave-uniform jumps, not exec masks
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), rg = w % kGRG,
+              ch = w / kGRG;
     const int ntiles_n = N / NTILE;
     const int total = m_off[E] * ntiles_n;
     const int range = (total + 7) >> 3;
