@@ -122,16 +122,16 @@ __global__ __launch_bounds__(256) void norm_matvec_kernel(const float *__restric
 //   MODE 1: x[r] += W[r] . a (wo + residual, rabbit2.c:500-501)
 //   MODE 2: out[r] = W[r] . (x * inv * nw), and the block's argmax candidate (largest value, first
 //           index) to cand[block] for argmax_cand_kernel (lm_head, rabbit2.c:545-546)
-template <int DT, int NC, int RPW, int MODE>
-__global__ __launch_bounds__(256) void dense_kernel(const float *__restrict__ x, const float *__restrict__ nw,
-                                                    float eps, Segs sg, int total_rows, float *__restrict__ resid,
-                                                    float2 *__restrict__ cand) {
+template <int DT, int NC, int RPW, int MODE, int WPB>
+__global__ __launch_bounds__(64 * WPB) void dense_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                         float eps, Segs sg, int total_rows, float *__restrict__ resid,
+                                                         float2 *__restrict__ cand) {
     constexpr int kPer = DT == RBT_DT_BF16 ? 8 : 4, kEsz = DT == RBT_DT_BF16 ? 2 : 4;
     constexpr int D = NC * kWave * kPer;
     __shared__ __align__(16) float xs[D];
     __shared__ float red[16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int r0 = (blockIdx.x * 4 + wv) * RPW;
+    const int r0 = (blockIdx.x * WPB + wv) * RPW;
     // weights first: row r0 + j (clamped into range; clamped rows are computed and dropped)
     u32x4 w[RPW][NC];
     int seg[RPW], row[RPW];
@@ -196,8 +196,8 @@ __global__ __launch_bounds__(256) void dense_kernel(const float *__restrict__ x,
         }
     }
     if constexpr (MODE == 2) {
-        __shared__ float s_b[4];
-        __shared__ int s_i[4];
+        __shared__ float s_b[WPB];
+        __shared__ int s_i[WPB];
         if (lane == 0) {
             s_b[wv] = best;
             s_i[wv] = bi;
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void dense_kernel(const float *__restrict__ x,
         if (threadIdx.x == 0) {
             float b = -INFINITY;
             int k = -1;
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < WPB; ++q)
                 if (s_i[q] >= 0 && (k < 0 || s_b[q] > b || (s_b[q] == b && s_i[q] < k))) {
                     b = s_b[q];
                     k = s_i[q];
@@ -334,17 +334,41 @@ __global__ __launch_bounds__(1024) void argmax_cand_kernel(const float2 *__restr
 }
 
 // ---------------------------------------------------------------- attention, split over positions
-// grid (n_heads, S). Block (h, s): QK-norm over the whole q and k projections (rabbit2.c:475-478), RoPE
-// of head h's q and of its kv head's k at pos (:479-480) from the [ctx][hd/2] (cos, sin) table, then the
-// positions t of its share of [0, pos]: scores q.k_t / sqrt(hd) (:486-492), and per wave an online
+// grid (n_heads, S, B). Block (h, s, b): QK-norm over the whole q and k projections (rabbit2.c:475-478),
+// RoPE of head h's q and of its kv head's k at pos (:479-480) from the [ctx][hd/2] (cos, sin) table, then
+// the positions t of its share of [0, pos]: scores q.k_t / sqrt(hd) (:486-492), and per wave an online
 // softmax (running max m, l = sum exp(score - m), o = sum exp(score - m) v_t) over its positions, the
 // K and V rows of KG positions in flight at once. The four waves merge into the block's partial
-// (m, l, o), which the wo kernel merges across the S splits (:493-498). The current position's k and v
-// come from registers; block (h, 0) of the first query head of each kv head appends them to the cache
+// (m, l, o), which attn_merge_kernel merges across the S splits (:493-498). The current position's k
+// and v come from LDS; block (h, 0) of the first query head of each kv head appends them to the cache
 // (:482-484).
-constexpr int kAttnMaxE = 4;  // head_dim <= 256: at most 4 elements per lane
+// Latency: after pos, every global load the block needs before its first scores (the norm inputs,
+// the head's q/k/v and norm weights, its RoPE entries, the first round of cached K/V rows) is issued
+// before any of them is used, and each later round's K/V rows are loaded during the previous round's
+// arithmetic.
+// AE = elements of a head row per lane (head_dim <= 64 AE).
+constexpr int kAttnMaxE = 4;  // head_dim <= 256
 constexpr int kAttnKG = 8;    // positions per wave per round
+constexpr int kAttnNU = 8;    // norm inputs per thread held in registers (q/k dims up to 2048 in one pass)
 
+template <int AE>
+__device__ __forceinline__ void attn_load_round(float (&kr)[kAttnKG][AE], float (&vr)[kAttnKG][AE],
+                                                const float *__restrict__ kc, const float *__restrict__ vc, int tb,
+                                                int t1, int kv_dim, int kvh, int hd, int lane) {
+#pragma unroll
+    for (int g = 0; g < kAttnKG; ++g) {
+        const int t = min(tb + g, t1 - 1);  // past the share: a repeat of the last row, weight 0 below
+        const float *kt = kc + (size_t)t * kv_dim + (size_t)kvh * hd, *vt = vc + (size_t)t * kv_dim + (size_t)kvh * hd;
+#pragma unroll
+        for (int e = 0; e < AE; ++e) {
+            const int i = lane + kWave * e;
+            kr[g][e] = i < hd ? kt[i] : 0.0f;
+            vr[g][e] = i < hd ? vt[i] : 0.0f;
+        }
+    }
+}
+
+template <int AE>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_raw, const float *__restrict__ k_raw,
                                                    const float *__restrict__ v_raw, const float *__restrict__ qw,
                                                    const float *__restrict__ kw, int qk_norm, float eps, int n_heads,
@@ -365,11 +389,46 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
     vc += (size_t)b * seq_stride;
     part += (size_t)b * n_heads * S * (hd + 2);
     const int pos = st[b].pos;
+
+    // ---- loads: norm inputs and this thread's element of the head (independent of pos) ...
+    float qa[kAttnNU], ka[kAttnNU];
+#pragma unroll
+    for (int u = 0; u < kAttnNU; ++u) {
+        const int i = tid + 256 * u;
+        qa[u] = qk_norm && i < q_dim ? q_raw[i] : 0.0f;
+        ka[u] = qk_norm && i < kv_dim ? k_raw[i] : 0.0f;
+    }
+    float qv = 0.0f, qwv = 0.0f, kv = 0.0f, kwv = 0.0f, vv = 0.0f;
+    if (tid < hd) {
+        const int qi = h * hd + tid, ki = kvh * hd + tid;
+        qv = q_raw[qi];
+        kv = k_raw[ki];
+        vv = v_raw[ki];
+        if (qk_norm) {
+            qwv = qw[qi];
+            kwv = kw[ki];
+        }
+    }
+    // ... then its RoPE entry and the first round of cached rows (pos is known by now)
+    const float2 cs = tid < half ? rope_cs[(size_t)pos * half + tid] : make_float2(0.0f, 0.0f);
+    const int n = pos + 1;
+    const int chunk = (n + S - 1) / S;
+    const int t0 = min(n, s * chunk), t1 = min(n, t0 + chunk);
+    float kr[kAttnKG][AE], vr[kAttnKG][AE];
+    const int tb0 = t0 + wv * kAttnKG;
+    if (tb0 < t1) attn_load_round(kr, vr, kc, vc, tb0, t1, kv_dim, kvh, hd, lane);
+
+    // ---- QK-norm: both sums of squares in one reduction (per thread in i = tid, tid + 256, ... order)
     float inv_q = 1.0f, inv_k = 1.0f;
-    if (qk_norm) {  // both sums of squares in one pass, one reduction
+    if (qk_norm) {
         float sq = 0.0f, sk = 0.0f;
-        for (int i = tid; i < q_dim; i += blockDim.x) sq += q_raw[i] * q_raw[i];
-        for (int i = tid; i < kv_dim; i += blockDim.x) sk += k_raw[i] * k_raw[i];
+#pragma unroll
+        for (int u = 0; u < kAttnNU; ++u) {
+            sq += qa[u] * qa[u];
+            sk += ka[u] * ka[u];
+        }
+        for (int i = tid + 256 * kAttnNU; i < q_dim; i += blockDim.x) sq += q_raw[i] * q_raw[i];
+        for (int i = tid + 256 * kAttnNU; i < kv_dim; i += blockDim.x) sk += k_raw[i] * k_raw[i];
         sq = wave_sum(sq);
         sk = wave_sum(sk);
         if (lane == 0) {
@@ -382,23 +441,21 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
         inv_q = 1.0f / sqrtf(sq / (float)q_dim + eps);
         inv_k = 1.0f / sqrtf(sk / (float)kv_dim + eps);
     }
-    for (int i = tid; i < hd; i += blockDim.x) {
-        const int qi = h * hd + i, ki = kvh * hd + i;
-        qh[i] = qk_norm ? q_raw[qi] * inv_q * qw[qi] : q_raw[qi];
-        kh[i] = qk_norm ? k_raw[ki] * inv_k * kw[ki] : k_raw[ki];
-        vh[i] = v_raw[ki];
+    if (tid < hd) {
+        qh[tid] = qk_norm ? qv * inv_q * qwv : qv;
+        kh[tid] = qk_norm ? kv * inv_k * kwv : kv;
+        vh[tid] = vv;
     }
     __syncthreads();
-    for (int i = tid; i < half; i += blockDim.x) {
+    if (tid < half) {
 #pragma clang fp contract(off)
-        const float2 cs = rope_cs[(size_t)pos * half + i];
-        float a = qh[i], b = qh[i + half];
-        qh[i] = a * cs.x - b * cs.y;
-        qh[i + half] = b * cs.x + a * cs.y;
-        a = kh[i];
-        b = kh[i + half];
-        kh[i] = a * cs.x - b * cs.y;
-        kh[i + half] = b * cs.x + a * cs.y;
+        float a = qh[tid], c = qh[tid + half];
+        qh[tid] = a * cs.x - c * cs.y;
+        qh[tid + half] = c * cs.x + a * cs.y;
+        a = kh[tid];
+        c = kh[tid + half];
+        kh[tid] = a * cs.x - c * cs.y;
+        kh[tid + half] = c * cs.x + a * cs.y;
     }
     __syncthreads();
     if (s == 0 && h % group == 0) {
@@ -408,38 +465,36 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
             vd[i] = vh[i];
         }
     }
-    const int n = pos + 1;
-    const int chunk = (n + S - 1) / S;
-    const int t0 = min(n, s * chunk), t1 = min(n, t0 + chunk);
     const float scale = 1.0f / sqrtf((float)hd);
-    float q[kAttnMaxE], o[kAttnMaxE];
+    float q[AE], o[AE];
 #pragma unroll
-    for (int e = 0; e < kAttnMaxE; ++e) {
+    for (int e = 0; e < AE; ++e) {
         const int i = lane + kWave * e;
         q[e] = i < hd ? qh[i] : 0.0f;
         o[e] = 0.0f;
     }
     float m = -INFINITY, l = 0.0f;
-    for (int tb = t0 + wv * kAttnKG; tb < t1; tb += 4 * kAttnKG) {  // wave-uniform rounds
-        float kr[kAttnKG][kAttnMaxE], vr[kAttnKG][kAttnMaxE];
+    for (int tb = tb0; tb < t1; tb += 4 * kAttnKG) {  // wave-uniform rounds
 #pragma unroll
         for (int g = 0; g < kAttnKG; ++g) {
-            const int t = min(tb + g, t1 - 1);  // past the share: a repeat of the last row, weight 0 below
-            const float *kt = t == pos ? kh : kc + (size_t)t * kv_dim + (size_t)kvh * hd;
-            const float *vt = t == pos ? vh : vc + (size_t)t * kv_dim + (size_t)kvh * hd;
+            if (min(tb + g, t1 - 1) == pos) {  // the current position: from LDS, not the cache
 #pragma unroll
-            for (int e = 0; e < kAttnMaxE; ++e) {
-                const int i = lane + kWave * e;
-                kr[g][e] = i < hd ? kt[i] : 0.0f;
-                vr[g][e] = i < hd ? vt[i] : 0.0f;
+                for (int e = 0; e < AE; ++e) {
+                    const int i = lane + kWave * e;
+                    kr[g][e] = i < hd ? kh[i] : 0.0f;
+                    vr[g][e] = i < hd ? vh[i] : 0.0f;
+                }
             }
         }
+        float kn[kAttnKG][AE], vn[kAttnKG][AE];
+        const int tn = tb + 4 * kAttnKG;
+        if (tn < t1) attn_load_round(kn, vn, kc, vc, tn, t1, kv_dim, kvh, hd, lane);  // the next round, in flight
         float sc[kAttnKG];
 #pragma unroll
         for (int g = 0; g < kAttnKG; ++g) {
             float d = 0.0f;
 #pragma unroll
-            for (int e = 0; e < kAttnMaxE; ++e) d += q[e] * kr[g][e];
+            for (int e = 0; e < AE; ++e) d += q[e] * kr[g][e];
             sc[g] = tb + g < t1 ? wave_sum(d) * scale : -INFINITY;
         }
         float mn = m;
@@ -448,15 +503,24 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
         const float alpha = expf(m - mn);  // m = -inf on the first round: alpha 0
         l *= alpha;
 #pragma unroll
-        for (int e = 0; e < kAttnMaxE; ++e) o[e] *= alpha;
+        for (int e = 0; e < AE; ++e) o[e] *= alpha;
 #pragma unroll
         for (int g = 0; g < kAttnKG; ++g) {
             const float p = expf(sc[g] - mn);  // positions past the share: exp(-inf) = 0
             l += p;
 #pragma unroll
-            for (int e = 0; e < kAttnMaxE; ++e) o[e] += p * vr[g][e];
+            for (int e = 0; e < AE; ++e) o[e] += p * vr[g][e];
         }
         m = mn;
+        if (tn < t1) {
+#pragma unroll
+            for (int g = 0; g < kAttnKG; ++g)
+#pragma unroll
+                for (int e = 0; e < AE; ++e) {
+                    kr[g][e] = kn[g][e];
+                    vr[g][e] = vn[g][e];
+                }
+        }
     }
     // merge the four waves
     if (lane == 0) {
@@ -464,7 +528,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
         w_l[wv] = l;
     }
 #pragma unroll
-    for (int e = 0; e < kAttnMaxE; ++e) {
+    for (int e = 0; e < AE; ++e) {
         const int i = lane + kWave * e;
         if (i < hd) w_o[wv][i] = o[e];
     }
@@ -773,7 +837,7 @@ hipError_t dense_dt(const Launch &L, int D, const float *x, const float *nw, flo
     switch (D / step) {
 #define DENSE_CASE(nc) \
     case nc:           \
-        return launch(L, dense_kernel<DT, nc, RPW, MODE>, g, b, 0, x, nw, eps, sg, total, resid, cand);
+        return launch(L, dense_kernel<DT, nc, RPW, MODE, 4>, g, b, 0, x, nw, eps, sg, total, resid, cand);
         DENSE_CASE(1)
         DENSE_CASE(2)
         DENSE_CASE(3)
@@ -915,8 +979,15 @@ hipError_t launch_attention(const Launch &L, const float *q, const float *k, con
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
                             float *part, int B) {
     if (hd > kWave * kAttnMaxE || S > 64) return hipErrorInvalidValue;
-    return launch(L, attn_kernel, dim3((unsigned)n_heads, (unsigned)S, (unsigned)B), dim3(256), 0, q, k, v, qw, kw,
-                  qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc, seq_stride, rope_cs, part);
+    const dim3 g((unsigned)n_heads, (unsigned)S, (unsigned)B), b(256);
+    if (hd <= kWave)
+        return launch(L, attn_kernel<1>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
+                      seq_stride, rope_cs, part);
+    if (hd <= 2 * kWave)
+        return launch(L, attn_kernel<2>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
+                      seq_stride, rope_cs, part);
+    return launch(L, attn_kernel<kAttnMaxE>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
+                  seq_stride, rope_cs, part);
 }
 
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B) {
