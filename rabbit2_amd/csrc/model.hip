@@ -132,7 +132,19 @@ __global__ __launch_bounds__(64 * WPB) void dense_kernel(const float *__restrict
     __shared__ float red[16];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int r0 = (blockIdx.x * WPB + wv) * RPW;
-    // weights first: row r0 + j (clamped into range; clamped rows are computed and dropped)
+    // the input vector (and norm weights) first: D / (64 WPB) elements per thread in i = tid, tid + 64 WPB,
+    // ... order; loads return in issue order, so the norm below waits for these and not for the
+    // weight rows, which stream in while the block reduces and stages x
+    constexpr int XU = (D + 64 * WPB - 1) / (64 * WPB);
+    float xr[XU], nr[XU];
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+        const int i = threadIdx.x + 64 * WPB * u;
+        xr[u] = i < D ? x[i] : 0.0f;
+        nr[u] = MODE == 1 || i >= D ? 0.0f : nw[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // then the weights: row r0 + j (clamped into range; clamped rows are computed and dropped)
     u32x4 w[RPW][NC];
     int seg[RPW], row[RPW];
 #pragma unroll
@@ -150,10 +162,18 @@ __global__ __launch_bounds__(64 * WPB) void dense_kernel(const float *__restrict
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (MODE == 1) {
-        for (int i = threadIdx.x; i < D; i += blockDim.x) xs[i] = x[i];
+#pragma unroll
+        for (int u = 0; u < XU; ++u)
+            if (threadIdx.x + 64 * WPB * u < D) xs[threadIdx.x + 64 * WPB * u] = xr[u];
     } else {
-        const float inv = rms_inv(x, D, eps, red);
-        for (int i = threadIdx.x; i < D; i += blockDim.x) xs[i] = x[i] * inv * nw[i];
+        float ss = 0.0f;  // rms_inv's per-thread order
+#pragma unroll
+        for (int u = 0; u < XU; ++u) ss += xr[u] * xr[u];
+        ss = block_sum(ss, red);
+        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int u = 0; u < XU; ++u)
+            if (threadIdx.x + 64 * WPB * u < D) xs[threadIdx.x + 64 * WPB * u] = xr[u] * inv * nr[u];
     }
     __syncthreads();
     float acc[RPW];
@@ -828,16 +848,24 @@ bool dense_ok(int dtype, int D, const void *const W[3], const int rows[3]) {
     return true;
 }
 
+// Launch shapes (rows per wave RPW, waves per block WPB), measured on the OLMoE shapes: the lm_head
+// (50304 rows) streams fastest with 2 rows per wave in 4-wave blocks; q/k/v (6144 rows) and wo (2048
+// rows) with one block of 8 waves per CU, 3 and 1 rows per wave.
+template <int MODE>
+struct DenseShape {
+    static constexpr int RPW = MODE == 2 ? 2 : MODE == 0 ? 3 : 1, WPB = MODE == 2 ? 4 : 8;
+};
+
 template <int DT, int MODE>
 hipError_t dense_dt(const Launch &L, int D, const float *x, const float *nw, float eps, const Segs &sg, int total,
                     float *resid, float2 *cand) {
     constexpr int step = DT == RBT_DT_BF16 ? 512 : 256;
-    constexpr int RPW = 4;
-    const dim3 g((unsigned)((total + 4 * RPW - 1) / (4 * RPW))), b(256);
+    constexpr int RPW = DenseShape<MODE>::RPW, WPB = DenseShape<MODE>::WPB;
+    const dim3 g((unsigned)((total + RPW * WPB - 1) / (RPW * WPB))), b(64 * WPB);
     switch (D / step) {
 #define DENSE_CASE(nc) \
     case nc:           \
-        return launch(L, dense_kernel<DT, nc, RPW, MODE, 4>, g, b, 0, x, nw, eps, sg, total, resid, cand);
+        return launch(L, dense_kernel<DT, nc, RPW, MODE, WPB>, g, b, 0, x, nw, eps, sg, total, resid, cand);
         DENSE_CASE(1)
         DENSE_CASE(2)
         DENSE_CASE(3)
@@ -957,7 +985,10 @@ hipError_t launch_dense_resid(const Launch &L, int dtype, const float *a, int co
     return launch_dense_mode<1>(L, dtype, cols, a, nullptr, 0.0f, sg, rows, x, nullptr);
 }
 
-int dense_argmax_blocks(int rows) { return (rows + 15) / 16; }
+int dense_argmax_blocks(int rows) {
+    constexpr int per = DenseShape<2>::RPW * DenseShape<2>::WPB;
+    return (rows + per - 1) / per;
+}
 
 hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const float *nw, float eps, int D,
                                const void *W, int rows, float *logits, float2 *cand, StepState *st, int32_t *seq,
