@@ -216,26 +216,39 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
     constexpr int WT = kDRows * 2 * G, XT = 2 * G;
     constexpr int WPER = (WT + 63) / 64, XPER = (XT + 63) / 64;
     u32x4 wv[WPER][8];
-    f32x4 xv[XPER][8][2];
+    f32x4 xv[XPER][8][2], nv[NORM ? XPER : 1][8][2];
+    auto load_w = [&]() {
 #pragma unroll
-    for (int q = 0; q < WPER; ++q) {
-        const int task = min(tid + 64 * q, WT - 1);
-        const int row = task / (2 * G), h = (task / G) & 1, g = task % G;
-        const int r = min(r0 + row, E - 1);
-        const uint16_t *src = W + (size_t)r * D + 8 * h;
+        for (int q = 0; q < WPER; ++q) {
+            const int task = min(tid + 64 * q, WT - 1);
+            const int row = task / (2 * G), h = (task / G) & 1, g = task % G;
+            const int r = min(r0 + row, E - 1);
+            const uint16_t *src = W + (size_t)r * D + 8 * h;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wv[q][i] = *reinterpret_cast<const u32x4 *>(src + 16 * (8 * g + i));
-    }
+            for (int i = 0; i < 8; ++i) wv[q][i] = *reinterpret_cast<const u32x4 *>(src + 16 * (8 * g + i));
+        }
+    };
+    // With NORM, x and the norm weights go before W: loads return in issue order, so the norm below
+    // waits for these only, while the router rows are still in flight. Without it W goes first.
+    if constexpr (!NORM) load_w();
 #pragma unroll
     for (int q = 0; q < XPER; ++q) {
         const int task = min(tid + 64 * q, XT - 1);
         const int h = task / G, g = task % G;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float *src = x + 16 * (8 * g + i) + 8 * h;
-            xv[q][i][0] = *reinterpret_cast<const f32x4 *>(src);
-            xv[q][i][1] = *reinterpret_cast<const f32x4 *>(src + 4);
+            const int off = 16 * (8 * g + i) + 8 * h;
+            xv[q][i][0] = *reinterpret_cast<const f32x4 *>(x + off);
+            xv[q][i][1] = *reinterpret_cast<const f32x4 *>(x + off + 4);
+            if constexpr (NORM) {
+                nv[q][i][0] = *reinterpret_cast<const f32x4 *>(nw + off);
+                nv[q][i][1] = *reinterpret_cast<const f32x4 *>(nw + off + 4);
+            }
         }
+    }
+    if constexpr (NORM) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_w();
     }
     if constexpr (NORM) {
         // sum of squares over the token's x (every element once: tasks past XT repeat the last one)
@@ -260,8 +273,7 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int off = 16 * (8 * g + i) + 8 * h;
-                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(nw + off);
-                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(nw + off + 4);
+                const f32x4 w0 = nv[q][i][0], w1 = nv[q][i][1];
                 f32x4 &a = xv[q][i][0], &b = xv[q][i][1];
                 a = f32x4{a.x * inv * w0.x, a.y * inv * w0.y, a.z * inv * w0.z, a.w * inv * w0.w};
                 b = f32x4{b.x * inv * w1.x, b.y * inv * w1.y, b.z * inv * w1.z, b.w * inv * w1.w};
