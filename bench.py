@@ -97,6 +97,8 @@ def main():
     ap.add_argument("--prefill-reps", type=int, default=20, help="timed calls per prefill workload")
     ap.add_argument("--no-full-model", action="store_true", help="skip the whole-model generate leg")
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode leg")
+    ap.add_argument("--profile-forward", type=int, default=0, metavar="N",
+                    help="only run N eager forward() steps of the whole model (for kernel traces) and exit")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one device-to-device copy of this size (a known-size kernel for scaling "
                          "FETCH_SIZE/WRITE_SIZE counters)")
@@ -106,6 +108,10 @@ def main():
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
               "multi-GPU sharding of the MoE layer is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
+
+    if args.profile_forward > 0:
+        profile_forward(args.profile_forward)
+        return
 
     from rabbit2_amd import hip as rh
 
@@ -314,12 +320,9 @@ FULL_MATS = ("wq", "wk", "wv", "wo", "router", "experts")
 FULL_NORMS = ("attn_norm", "q_norm", "k_norm", "ffn_norm")
 
 
-def full_model_leg(with_cpu, cpu_seconds, batched=True):
-    """128 random prompt ids, then 256 greedy tokens through rbt_hip_generate (one HIP graph replay
-    per token, the argmax feeding the next step on the device). Reports generated tok/s, prompt tok/s
-    and the weight bytes streamed per generated token."""
+def make_full_model(dev):
+    """The random-init model of FULL_CFG in a fresh device image; returns (cfg, seconds)."""
     from rabbit2_amd import hip as rh
-    dev = rh.Device(0)
     cfg = rh.Config(**FULL_CFG)
     t0 = time.time()
     base = dev.model_create(cfg)
@@ -341,7 +344,16 @@ def full_model_leg(with_cpu, cpu_seconds, batched=True):
     fill_tensor("final_norm", 0, rh.DT_F32, 0.0, 1.0)
     fill_tensor("lm_head", 0, rh.DT_BF16, W_SCALE, 0.0)
     dev.synchronize()
-    setup_s = time.time() - t0
+    return cfg, time.time() - t0
+
+
+def full_model_leg(with_cpu, cpu_seconds, batched=True):
+    """128 random prompt ids, then 256 greedy tokens through rbt_hip_generate (one HIP graph replay
+    per token, the argmax feeding the next step on the device). Reports generated tok/s, prompt tok/s
+    and the weight bytes streamed per generated token."""
+    from rabbit2_amd import hip as rh
+    dev = rh.Device(0)
+    cfg, setup_s = make_full_model(dev)
     dev.set_router_order(rh.ORDER_AVX2)
     dev.state_init(N_PROMPT + N_GEN)
     prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, N_PROMPT).astype(np.int32)
@@ -378,6 +390,24 @@ def full_model_leg(with_cpu, cpu_seconds, batched=True):
         res["batched_decode"] = batched_leg(dev, cfg)
     dev.close()
     return res
+
+
+def profile_forward(steps):
+    """`steps` eager rbt_hip_forward calls of the whole model over random prompt ids (positions 0 ..
+    steps-1), for kernel traces: no HIP graphs, no bench line."""
+    from rabbit2_amd import hip as rh
+    dev = rh.Device(0)
+    cfg, _ = make_full_model(dev)
+    dev.set_router_order(rh.ORDER_AVX2)
+    dev.state_init(max(steps, 1))
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, steps).astype(np.int32)
+    t0 = time.perf_counter()
+    for p in range(steps):
+        dev.forward(int(prompt[p]), p, cfg.vocab, cfg.n_layers, cfg.top_k)
+    dev.synchronize()
+    print(f"profile-forward: {steps} eager forward steps of the 16-layer model in {time.perf_counter() - t0:.3f} s",
+          file=sys.stderr, flush=True)
+    dev.close()
 
 
 B_SEQ, B_CTX, B_GEN = 32, 2048, 64
