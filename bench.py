@@ -99,6 +99,8 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode leg")
     ap.add_argument("--profile-forward", type=int, default=0, metavar="N",
                     help="only run N eager forward() steps of the whole model (for kernel traces) and exit")
+    ap.add_argument("--profile-batch", type=int, default=0, metavar="B",
+                    help="with --profile-forward: B sequences per step at the batched leg's context length")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run one device-to-device copy of this size (a known-size kernel for scaling "
                          "FETCH_SIZE/WRITE_SIZE counters)")
@@ -110,7 +112,7 @@ def main():
         sys.exit(2)
 
     if args.profile_forward > 0:
-        profile_forward(args.profile_forward)
+        profile_forward(args.profile_forward, args.profile_batch)
         return
 
     from rabbit2_amd import hip as rh
@@ -392,21 +394,30 @@ def full_model_leg(with_cpu, cpu_seconds, batched=True):
     return res
 
 
-def profile_forward(steps):
-    """`steps` eager rbt_hip_forward calls of the whole model over random prompt ids (positions 0 ..
-    steps-1), for kernel traces: no HIP graphs, no bench line."""
+def profile_forward(steps, batch):
+    """`steps` eager forward steps of the whole model over random ids, for kernel traces (no HIP graphs,
+    no bench line). batch 0: rbt_hip_forward at positions 0 .. steps-1; batch B > 0: rbt_hip_forward_batch
+    of B sequences at positions B_CTX .. B_CTX + steps - 1 of the batched leg's context (the caches
+    below hold the zeros of batch_init instead of a filled context; the kernels read the same bytes)."""
     from rabbit2_amd import hip as rh
     dev = rh.Device(0)
     cfg, _ = make_full_model(dev)
     dev.set_router_order(rh.ORDER_AVX2)
-    dev.state_init(max(steps, 1))
-    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, steps).astype(np.int32)
+    rng = np.random.default_rng(SEED)
     t0 = time.perf_counter()
-    for p in range(steps):
-        dev.forward(int(prompt[p]), p, cfg.vocab, cfg.n_layers, cfg.top_k)
+    if batch <= 0:
+        dev.state_init(max(steps, 1))
+        prompt = rng.integers(0, cfg.vocab, steps).astype(np.int32)
+        for p in range(steps):
+            dev.forward(int(prompt[p]), p, cfg.vocab, cfg.n_layers, cfg.top_k)
+    else:
+        dev.batch_init(batch, B_CTX + steps)
+        for p in range(steps):
+            toks = rng.integers(0, cfg.vocab, batch).astype(np.int32)
+            dev.forward_batch(toks, np.full(batch, B_CTX + p, np.int32), cfg.vocab, cfg.n_layers, cfg.top_k)
     dev.synchronize()
-    print(f"profile-forward: {steps} eager forward steps of the 16-layer model in {time.perf_counter() - t0:.3f} s",
-          file=sys.stderr, flush=True)
+    print(f"profile-forward: {steps} eager steps of the 16-layer model (batch {max(batch, 1)}) in "
+          f"{time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
     dev.close()
 
 

@@ -266,11 +266,26 @@ __global__ __launch_bounds__(256) void dense_batch_kernel(const float *__restric
 #pragma unroll
         for (int i = 0; i < NC; ++i) w[j][i] = ld_stream_u4(src + (size_t)(lane + kWave * i) * 16);
     }
+    constexpr int UPT = (TB * D / 4 + 255) / 256;  // 16-byte staging units per thread for a full chunk
     for (int b0 = 0; b0 < B; b0 += TB) {  // block-uniform
         const int nb = B - b0 < TB ? B - b0 : TB;
+        const int nu = nb * D / 4;
+        // the chunk's token rows: every load issued before the first store (indices clamped, so the
+        // loads carry no branches)
+        f32x4 sv[UPT];
+        const f32x4 *src4 = reinterpret_cast<const f32x4 *>(xin + (size_t)b0 * D);
+#pragma unroll
+        for (int k = 0; k < UPT; ++k) sv[k] = src4[min((int)threadIdx.x + 256 * k, nu - 1)];
         __syncthreads();  // the previous chunk's reads are done
-        for (int i = threadIdx.x; i < nb * D; i += blockDim.x) xs[i] = xin[(size_t)b0 * D + i];
+#pragma unroll
+        for (int k = 0; k < UPT; ++k) {
+            const int u = threadIdx.x + 256 * k;
+            if (u < nu) reinterpret_cast<f32x4 *>(xs)[u] = sv[k];
+        }
         __syncthreads();
+        float res[RPW];  // lane tt keeps token b0 + tt's sums
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) res[j] = 0.0f;
         for (int tt = 0; tt < nb; ++tt) {
             const float *xt = xs + tt * D;
 #pragma unroll
@@ -290,16 +305,24 @@ __global__ __launch_bounds__(256) void dense_batch_kernel(const float *__restric
                                __uint_as_float(v.z) * x0.z + __uint_as_float(v.w) * x0.w;
                     }
                 }
-                const float sum = wave_sum(acc);
-                if (lane == 0 && r0 + j < total_rows) {
-                    const size_t b = (size_t)(b0 + tt);
-                    if constexpr (MODE == 1) {
-                        float *o = resid + b * total_rows + row[j];
-                        *o = *o + sum;
-                    } else {
-                        sg.out[seg[j]][b * sg.rows[seg[j]] + row[j]] = sum;
-                    }
-                }
+                const float sum = wave_sum(acc);  // wave-uniform
+                if (lane == tt) res[j] = sum;
+            }
+        }
+        // the chunk's outputs: lane tt writes token b0 + tt's rows (residual reads first, all in flight)
+        if (lane < nb) {
+            const size_t b = (size_t)(b0 + lane);
+            if constexpr (MODE == 1) {
+                float old[RPW];
+#pragma unroll
+                for (int j = 0; j < RPW; ++j) old[j] = resid[b * total_rows + row[j]];
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+                    if (r0 + j < total_rows) resid[b * total_rows + row[j]] = old[j] + res[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < RPW; ++j)
+                    if (r0 + j < total_rows) sg.out[seg[j]][b * sg.rows[seg[j]] + row[j]] = res[j];
             }
         }
     }
