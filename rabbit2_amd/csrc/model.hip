@@ -601,10 +601,18 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     const int h = blockIdx.x, b = blockIdx.y, n_heads = gridDim.x;
     const float *ph = part + ((size_t)b * n_heads + h) * S * (hd + 2);
     ao += (size_t)b * n_heads * hd;
+    // loads first: this thread's element of splits 0..15 (clamped indices, no branches) and wave 0's
+    // (m, l) of split q = lane
+    const int ie = min((int)threadIdx.x, hd - 1);
+    float ov[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) ov[q] = ph[(size_t)min(q, S - 1) * (hd + 2) + 2 + ie];
+    const int qc = min((int)threadIdx.x & 63, S - 1);
+    const float pm = ph[(size_t)qc * (hd + 2)], pl = ph[(size_t)qc * (hd + 2) + 1];
     if (threadIdx.x < 64) {  // S <= 64 split weights, by wave 0
         const int q = threadIdx.x;
-        const float m = q < S ? ph[(size_t)q * (hd + 2)] : -INFINITY;
-        const float l = q < S ? ph[(size_t)q * (hd + 2) + 1] : 0.0f;
+        const float m = q < S ? pm : -INFINITY;
+        const float l = q < S ? pl : 0.0f;
         const float M = wave_max(m);
         const float a = l > 0.0f ? expf(m - M) : 0.0f;
         wa[q] = a;
@@ -612,9 +620,13 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
         if (q == 0) s_inv = 1.0f / L;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+    const int i = threadIdx.x;  // hd <= blockDim.x
+    if (i < hd) {
         float o = 0.0f;
-        for (int q = 0; q < S; ++q) o += wa[q] * ph[(size_t)q * (hd + 2) + 2 + i];
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+            if (q < S) o += wa[q] * ov[q];
+        for (int q = 16; q < S; ++q) o += wa[q] * ph[(size_t)q * (hd + 2) + 2 + i];
         ao[(size_t)h * hd + i] = o * s_inv;
     }
 }
@@ -641,8 +653,28 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
     __shared__ float red[16];
     x += (size_t)blockIdx.x * n;  // one row per block
     out += (size_t)blockIdx.x * n;
-    const float inv = rms_inv(x, n, eps, red);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
+    // rows of up to 4 * 1024 elements from registers (x and w loaded together), longer ones by the loop
+    constexpr int U = 4;
+    float xr[U], wr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = min((int)threadIdx.x + 1024 * u, n - 1);
+        xr[u] = x[i];
+        wr[u] = w[i];
+    }
+    float ss = 0.0f;  // rms_inv's per-thread order
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if ((int)threadIdx.x + 1024 * u < n) ss += xr[u] * xr[u];
+    for (int i = threadIdx.x + 1024 * U; i < n; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = threadIdx.x + 1024 * u;
+        if (i < n) out[i] = xr[u] * inv * wr[u];
+    }
+    for (int i = threadIdx.x + 1024 * U; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
 }
 
 // ---------------------------------------------------------------- greedy argmax (rabbit2.c:552-556)
@@ -658,13 +690,32 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
     seq += (size_t)blockIdx.x * ctx;
     float best = -INFINITY;
     int idx = n;  // n: nothing found yet
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float a = v[i];
+    auto visit = [&](float a, int i) {
         if (a == a && (idx == n || a > best)) {  // first non-NaN, then strictly larger
             best = a;
             idx = i;
         }
+    };
+    // each thread visits its indices in ascending order: 16-byte chunks c = tid, tid + 1024, ... (four
+    // in flight per round, indices clamped), then the tail past the last whole chunk
+    const int n4 = (n % 4 == 0) ? n / 4 : 0;
+    const f32x4 *v4 = reinterpret_cast<const f32x4 *>(v);
+    for (int c0 = threadIdx.x; c0 < n4; c0 += 4 * 1024) {
+        f32x4 a[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = v4[min(c0 + 1024 * j, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = c0 + 1024 * j;
+            if (c < n4) {
+                visit(a[j].x, 4 * c);
+                visit(a[j].y, 4 * c + 1);
+                visit(a[j].z, 4 * c + 2);
+                visit(a[j].w, 4 * c + 3);
+            }
+        }
     }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) visit(v[i], i);
     // wave then block reduction on (value, index): larger value wins, equal values keep the lower index
     for (int off = 32; off > 0; off >>= 1) {
         const float ob = __shfl_down(best, off, 64);

@@ -359,16 +359,35 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restri
     const int t = blockIdx.y;
     const int d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= D) return;
-    float moe = 0.0f;
-    for (int k = 0; k < K; ++k) {
-#pragma clang fp contract(off)
-        const float tmp = y[(size_t)pos_of[t * K + k] * D + d];
-        const float wk = weights[t * K + k];
-        moe = moe + wk * tmp;
-    }
     const size_t o = (size_t)t * D + d;
+    const float xo = x_inout ? x_inout[o] : 0.0f;
+    float moe = 0.0f;
+    if (K <= 8) {  // the common case: every load of the row issued before the sum (indices clamped)
+        int p[8];
+        float wk[8], tmp[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int kc = min(k, K - 1);
+            p[k] = pos_of[t * K + kc];
+            wk[k] = weights[t * K + kc];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) tmp[k] = y[(size_t)p[k] * D + d];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+#pragma clang fp contract(off)
+            if (k < K) moe = moe + wk[k] * tmp[k];
+        }
+    } else {
+        for (int k = 0; k < K; ++k) {
+#pragma clang fp contract(off)
+            const float tmp = y[(size_t)pos_of[t * K + k] * D + d];
+            const float wk = weights[t * K + k];
+            moe = moe + wk * tmp;
+        }
+    }
     if (moe_out) moe_out[o] = moe;
-    if (x_inout) x_inout[o] = x_inout[o] + moe;
+    if (x_inout) x_inout[o] = xo + moe;
 }
 
 template <int MATS>
