@@ -115,7 +115,7 @@ def main():
         profile_forward(args.profile_forward, args.profile_batch)
         return
 
-    from rabbit2_amd import hip as rh
+    from rabbitm2_amd import hip as rh
 
     dev = rh.Device(0)
     esz = 2
@@ -324,7 +324,7 @@ FULL_NORMS = ("attn_norm", "q_norm", "k_norm", "ffn_norm")
 
 def make_full_model(dev):
     """The random-init model of FULL_CFG in a fresh device image; returns (cfg, seconds)."""
-    from rabbit2_amd import hip as rh
+    from rabbitm2_amd import hip as rh
     cfg = rh.Config(**FULL_CFG)
     t0 = time.time()
     base = dev.model_create(cfg)
@@ -353,7 +353,7 @@ def full_model_leg(with_cpu, cpu_seconds, batched=True):
     """128 random prompt ids, then 256 greedy tokens through rbt_hip_generate (one HIP graph replay
     per token, the argmax feeding the next step on the device). Reports generated tok/s, prompt tok/s
     and the weight bytes streamed per generated token."""
-    from rabbit2_amd import hip as rh
+    from rabbitm2_amd import hip as rh
     dev = rh.Device(0)
     cfg, setup_s = make_full_model(dev)
     dev.set_router_order(rh.ORDER_AVX2)
@@ -399,7 +399,7 @@ def profile_forward(steps, batch):
     no bench line). batch 0: rbt_hip_forward at positions 0 .. steps-1; batch B > 0: rbt_hip_forward_batch
     of B sequences at positions B_CTX .. B_CTX + steps - 1 of the batched leg's context (the caches
     below hold the zeros of batch_init instead of a filled context; the kernels read the same bytes)."""
-    from rabbit2_amd import hip as rh
+    from rabbitm2_amd import hip as rh
     dev = rh.Device(0)
     cfg, _ = make_full_model(dev)
     dev.set_router_order(rh.ORDER_AVX2)
@@ -497,7 +497,7 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
     plain router and once with +2.0 on the router logits of experts 0-7 (skewed load). Reports the
     per-call time, per-kernel times (HIP events), the tokens-per-expert histogram of the dispatch,
     the layer's algorithmic HBM rate and the grouped GEMMs' matrix-core utilisation."""
-    from rabbit2_amd import hip as rh
+    from rabbitm2_amd import hip as rh
     T = PREFILL_T
     P = T * K
     xraw = dev.malloc(T * D * 2)

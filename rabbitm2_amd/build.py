@@ -1,9 +1,9 @@
 """Builds librbt2_hip.so (the C-ABI of include/rbt2_hip.h) for gfx950 with hipcc, in-tree.
 
-    python -m rabbit2_amd.build          # or rabbit2_amd.build.build()
+    python -m rabbitm2_amd.build          # or rabbitm2_amd.build.build()
 
 Every .hip under csrc/ is compiled to an object in _build/ (in parallel) and linked into
-rabbit2_amd/librbt2_hip.so. Always recompiles: the driver uses this as its "does it build" check.
+rabbitm2_amd/librbt2_hip.so. Always recompiles: the driver uses this as its "does it build" check.
 """
 import concurrent.futures as cf
 import os

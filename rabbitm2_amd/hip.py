@@ -51,7 +51,7 @@ def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
-            raise HipError(f"{LIB_PATH} is missing: build it with `python -m rabbit2_amd.build`")
+            raise HipError(f"{LIB_PATH} is missing: build it with `python -m rabbitm2_amd.build`")
         L = C.CDLL(LIB_PATH)
         vp, i32, u64, f32 = C.c_void_p, C.c_int, C.c_uint64, C.c_float
         L.rbt_hip_init.argtypes = [C.POINTER(vp), i32]

@@ -72,7 +72,7 @@ class SynthLayer:
         self.bias_dev = None if bias is None else dev.upload_array(self.bias)
 
     def desc(self):
-        from rabbit2_amd.hip import moe_layer_desc
+        from rabbitm2_amd.hip import moe_layer_desc
         return moe_layer_desc(self.D, self.E, self.K, self.H, self.dtype, self.norm_topk, self.router_dev,
                               self.experts_dev, self.stride, self.bias_dev)
 

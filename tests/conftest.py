@@ -16,7 +16,7 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def dev():
     """One rbt_hip handle on cuda device 0 for the whole GPU session."""
-    from rabbit2_amd.hip import Device
+    from rabbitm2_amd.hip import Device
     d = Device(0)
     yield d
     d.close()

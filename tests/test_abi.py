@@ -7,7 +7,7 @@ import subprocess
 
 import pytest
 
-from rabbit2_amd import hip
+from rabbitm2_amd import hip
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "rbt2_hip.h")

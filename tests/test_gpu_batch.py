@@ -99,7 +99,7 @@ def test_generate_batch_matches_each_sequence_alone(dev, case, B):
 
 
 def test_batch_arguments_checked(dev):
-    from rabbit2_amd.hip import HipError
+    from rabbitm2_amd.hip import HipError
     spec, cfg, model = build("ref_bf16")
     dev.upload(model)
     dev.batch_init(2, 8)

@@ -96,7 +96,7 @@ def test_generate_stops_after_eos_and_clamps_to_context(dev):
 
 
 def test_forward_rejects_bad_arguments(dev):
-    from rabbit2_amd.hip import HipError
+    from rabbitm2_amd.hip import HipError
     spec, cfg, model = build("ref_bf16")
     dev.upload(model)
     with pytest.raises(HipError):

@@ -67,7 +67,7 @@ def test_upload_file_matches_the_file_and_the_reference(dev, tmp_path, case):
 
 
 def test_upload_file_rejects_bad_files(dev, tmp_path):
-    from rabbit2_amd.hip import HipError
+    from rabbitm2_amd.hip import HipError
     spec, cfg, model = build("ref_bf16")
     with pytest.raises(HipError, match="cannot open"):
         dev.upload_file(str(tmp_path / "missing.rbt2"))

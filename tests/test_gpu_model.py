@@ -54,7 +54,7 @@ def test_upload_moe_matvec(dev, name):
 
 
 def test_upload_rejects_bad_images(dev):
-    from rabbit2_amd.hip import HipError
+    from rabbitm2_amd.hip import HipError
     cfg, gp = MODELS["bf16_renorm"]
     model = po.build_model(cfg, gp)
     bad = model.copy()

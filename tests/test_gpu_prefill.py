@@ -1,7 +1,7 @@
 """Parity of the grouped (prefill) MoE path: dispatch, MFMA gate/up and down GEMMs, combine.
 
 Many tokens per call go through per-expert lists instead of per-(token, slot) GEMVs
-(rabbit2_amd/csrc/prefill.hip). The engine evaluates them one token at a time
+(rabbitm2_amd/csrc/prefill.hip). The engine evaluates them one token at a time
 (rabbit2/src/rabbit2.c:703-714, MoE block :511-542); per token the result must meet the same bar as
 decode: routing identical except at exact CPU ties, normwise max error <= 1e-3 (tests/common.py).
 The tokens-per-expert histogram must equal the count of the oracle's routing exactly.
