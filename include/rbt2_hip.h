@@ -81,6 +81,12 @@ int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config 
  * maps the file read-only and copies the image to HBM once, sequentially (replaces map_file and
  * get_expert's reads, rabbit2.c:129-156, :261-300). Fills *cfg (may be NULL). */
 int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg);
+/* Host only (no device needed): reads the header of a .rbt2 file and validates it like load_model()
+ * (rabbit2.c:199-228), the file included (it must hold its own layout), then reports what --info
+ * prints (rabbit2.c:668-679): *cfg (may be NULL) and info (may be NULL) = {tok_emb, layer0_experts,
+ * last_layer_experts, expert_stride, lm_head, layout_end, file_size} in bytes, from the layout rules
+ * of rabbit2.c:158-193. Errors go to rbt_hip_last_error(NULL). */
+int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]);
 /* The engine's expert-cache counters (rabbit2.c:745-751) for the HBM-resident image:
  * stats = {hits, misses, evictions, bytes_read, resident_bytes, capacity_bytes}. Every expert is a
  * miss once (read at upload) and stays resident: evictions 0, bytes_read = misses * expert_stride,

@@ -1,4 +1,5 @@
-"""Builds librbt2_hip.so (the C-ABI of include/rbt2_hip.h) for gfx950 with hipcc, in-tree.
+"""Builds librbt2_hip.so (the C-ABI of include/rbt2_hip.h) for gfx950 with hipcc, in-tree, and the
+engine's command line over it (rabbitm2_amd/rabbit2, C99, from host/rabbit2_main.c).
 
     python -m rabbitm2_amd.build          # or rabbitm2_amd.build.build()
 
@@ -16,6 +17,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "librbt2_hip.so")
+CLI = os.path.join(PKG, "rabbit2")
+CLI_SRC = os.path.join(PKG, "host", "rabbit2_main.c")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -60,7 +63,23 @@ def build(verbose=False):
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_cli()
     return LIB
+
+
+def build_cli():
+    """The engine's CLI: plain C99 linked against the library (found next to it at run time)."""
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler found for the rabbit2 command line")
+    tmp = CLI + ".tmp"
+    cmd = [cc, "-O2", "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"), CLI_SRC,
+           "-L", PKG, "-lrbt2_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"building the rabbit2 command line failed:\n{res.stderr}")
+    os.replace(tmp, CLI)
+    return CLI
 
 
 if __name__ == "__main__":

@@ -279,6 +279,25 @@ bool config_ok(const rbt_config &c) {
              (c.dtype != RBT_DT_F32 && c.dtype != RBT_DT_BF16));
 }
 
+// The header checks of load_model (rabbit2.c:199-228) on the first bytes of a file of file_size
+// bytes: magic, version 2, a valid config, and a file at least as long as its own layout. On success
+// h->cfg and the layout fields hold the file's (h may be a host-only handle).
+int parse_header(rbt_hip *h, const unsigned char *d, uint64_t file_size, rbt_hip *err_h) {
+    if (!d || file_size < kHeader || memcmp(d, "RBT2", 4) != 0) return fail(err_h, "bad magic: not a .rbt2 file");
+    uint32_t version;
+    memcpy(&version, d + 4, 4);
+    if (version != 2) return fail(err_h, "unsupported .rbt2 version %u (need 2)", version);
+    rbt_config c;
+    memcpy(&c, d + 8, sizeof c);
+    if (!config_ok(c)) return fail(err_h, "invalid config in header");
+    h->cfg = c;
+    compute_layout(h);
+    if (h->layout_end > file_size)
+        return fail(err_h, "file too small for its own config (%llu < %llu)", (unsigned long long)file_size,
+                    (unsigned long long)h->layout_end);
+    return 1;
+}
+
 // (Re)allocates the device image for h->cfg's layout; drops any decode state of an earlier model.
 int model_alloc(rbt_hip *h) {
     if (!set_device(h)) return 0;
@@ -477,19 +496,8 @@ int rbt_hip_set_router_order(rbt_hip *h, int order) {
 
 int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config *cfg) {
     if (!h) return fail(nullptr, "upload: handle is NULL");
-    const unsigned char *d = static_cast<const unsigned char *>(file);
-    if (!d || file_size < kHeader || memcmp(d, "RBT2", 4) != 0) return fail(h, "bad magic: not a .rbt2 file");
-    uint32_t version;
-    memcpy(&version, d + 4, 4);
-    if (version != 2) return fail(h, "unsupported .rbt2 version %u (need 2)", version);
-    rbt_config c;
-    memcpy(&c, d + 8, sizeof c);
-    if (!config_ok(c)) return fail(h, "invalid config in header");
-    h->cfg = c;
-    compute_layout(h);
-    if (h->layout_end > file_size)
-        return fail(h, "file too small for its own config (%llu < %llu)", (unsigned long long)file_size,
-                    (unsigned long long)h->layout_end);
+    if (!parse_header(h, static_cast<const unsigned char *>(file), file_size, h)) return 0;
+    const rbt_config c = h->cfg;
     if (!model_alloc(h)) return 0;
     HIP_OK(h, hipMemcpy(h->model, file, h->layout_end, hipMemcpyHostToDevice));
     h->cache_hits = 0;
@@ -511,19 +519,10 @@ int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
     if (fstat(fd, &st) != 0) return fail(h, "cannot stat %s", path);
     const uint64_t file_size = (uint64_t)st.st_size;
     unsigned char hdr[kHeader];
-    if (file_size < kHeader || pread(fd, hdr, kHeader, 0) != (ssize_t)kHeader || memcmp(hdr, "RBT2", 4) != 0)
+    if (file_size < kHeader || pread(fd, hdr, kHeader, 0) != (ssize_t)kHeader)
         return fail(h, "bad magic: not a .rbt2 file");
-    uint32_t version;
-    memcpy(&version, hdr + 4, 4);
-    if (version != 2) return fail(h, "unsupported .rbt2 version %u (need 2)", version);
-    rbt_config c;
-    memcpy(&c, hdr + 8, sizeof c);
-    if (!config_ok(c)) return fail(h, "invalid config in header");
-    h->cfg = c;
-    compute_layout(h);
-    if (h->layout_end > file_size)
-        return fail(h, "file too small for its own config (%llu < %llu)", (unsigned long long)file_size,
-                    (unsigned long long)h->layout_end);
+    if (!parse_header(h, hdr, file_size, h)) return 0;
+    const rbt_config c = h->cfg;
     if (!model_alloc(h)) return 0;
     // the file mapped read-only (rabbit2.c:141-147) and copied in one call: the runtime pipelines a
     // pageable source through its own pinned staging (measured ~29 GB/s from the page cache, three
@@ -547,6 +546,35 @@ int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
+    return 1;
+}
+
+int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]) {
+    if (!path) return fail(nullptr, "file_info: path is NULL");
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return fail(nullptr, "cannot open %s", path);  // rabbit2.c:200
+    struct FdCloser {
+        int fd;
+        ~FdCloser() { close(fd); }
+    } closer{fd};
+    struct stat st;
+    if (fstat(fd, &st) != 0) return fail(nullptr, "cannot stat %s", path);
+    const uint64_t file_size = (uint64_t)st.st_size;
+    unsigned char hdr[kHeader];
+    if (file_size < kHeader || pread(fd, hdr, kHeader, 0) != (ssize_t)kHeader)
+        return fail(nullptr, "bad magic: not a .rbt2 file");
+    rbt_hip tmp;  // host-only: no device, no stream
+    if (!parse_header(&tmp, hdr, file_size, nullptr)) return 0;
+    if (cfg) *cfg = tmp.cfg;
+    if (info) {
+        info[0] = tmp.tok_emb;
+        info[1] = tmp.layers.front().experts;
+        info[2] = tmp.layers.back().experts;
+        info[3] = tmp.expert_stride;
+        info[4] = tmp.lm_head;
+        info[5] = tmp.layout_end;
+        info[6] = file_size;
+    }
     return 1;
 }
 

@@ -22,7 +22,7 @@ EXPORTS = (
     "rbt_hip_memset_dev", "rbt_hip_synchronize", "rbt_hip_stream", "rbt_hip_fill_normal", "rbt_hip_profile_enable",
     "rbt_hip_profile_get", "rbt_hip_set_option", "rbt_hip_state_init", "rbt_hip_forward", "rbt_hip_generate",
     "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
-    "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling",
+    "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling", "rbt_hip_file_info",
 )
 
 

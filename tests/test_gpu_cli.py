@@ -1,0 +1,101 @@
+"""The engine's command line over the C ABI (rabbitm2_amd/rabbit2) on the GPU, run exactly as the
+reference's own tests run the engine binary (rabbit2/tests/test_forward.py:53-66,
+test_engine_cache.py:33-58): --dump files and --gen ids against the reference engine's outputs for the
+same arguments (the golden fixtures, tests/golden/make_golden.py and make_sampled.py).
+
+Bar: the routing file identical, logits normwise max error <= 1e-3 per position, ids identical (greedy
+and sampled); the expert-cache line keeps the engine's bytes_read == misses * expert_stride."""
+import json
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+from tests.common import normwise_err
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "rabbitm2_amd", "rabbit2")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+MANIFEST = json.load(open(os.path.join(GOLDEN, "manifest.json")))["cases"]
+SAMPLED = json.load(open(os.path.join(GOLDEN, "sampled.json")))
+KERNEL_FLAGS = {"scalar": [], "avx2": ["--kernel", "avx2"]}  # the orders the fixtures were written in
+LOGIT_RTOL = 1e-3
+
+
+def write_case(case, tmp_path):
+    spec = MANIFEST[case]
+    cfg = po.Config(**spec["config"])
+    g = spec["gen_params"]
+    path = tmp_path / f"{case}.rbt2"
+    po.write_model(str(path), cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                                emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    return spec, cfg, path
+
+
+def run(*args):
+    print("rabbit2", " ".join(str(a) for a in args[1:]), flush=True)
+    res = subprocess.run([CLI] + [str(a) for a in args], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    return res.stdout, res.stderr
+
+
+@pytest.mark.parametrize("case", sorted(MANIFEST))
+def test_cli_dump_and_gen_match_reference(tmp_path, case):
+    spec, cfg, path = write_case(case, tmp_path)
+    fx = np.load(os.path.join(GOLDEN, case + ".npz"))
+    tokens = [int(t) for t in fx["tokens"]]
+    for tag, flags in KERNEL_FLAGS.items():
+        lp, rp = tmp_path / "logits.bin", tmp_path / "routing.bin"
+        out, err = run(path, "--dump", lp, rp, *flags, *tokens)
+        assert "prompt: %d tokens" % len(tokens) in err
+        logits = np.fromfile(lp, dtype="<f4").reshape(len(tokens), cfg.vocab)
+        routing = np.fromfile(rp, dtype="<i4").reshape(len(tokens), cfg.n_layers, cfg.top_k)
+        assert np.array_equal(routing, fx[f"routing_{tag}"]), f"{case} {tag}"
+        for pos in range(len(tokens)):
+            assert normwise_err(logits[pos], fx[f"logits_{tag}"][pos]) <= LOGIT_RTOL, f"{case} {tag} pos {pos}"
+        out, err = run(path, "--gen", spec["n_gen"], *flags, *tokens)
+        assert [int(t) for t in out.split()] == fx[f"gen_{tag}"].tolist(), f"{case} {tag}"
+        assert "generated %d in" % spec["n_gen"] in err
+
+
+@pytest.mark.parametrize("case", sorted(SAMPLED["cases"]))
+def test_cli_sampled_gen_matches_reference(tmp_path, case):
+    spec, cfg, path = write_case(case, tmp_path)
+    fx = np.load(os.path.join(GOLDEN, "sampled.npz"))
+    tokens = po.prompt_tokens(spec["gen_params"]["seed"], spec["n_prompt"], cfg.vocab)
+    n_gen = SAMPLED["cases"][case]["n_gen"]
+    for j, (t, k, p, seed) in enumerate(SAMPLED["settings"]):
+        for tag, flags in KERNEL_FLAGS.items():
+            out, _ = run(path, "--gen", n_gen, "--temperature", t, "--top-k", k, "--top-p", p, "--seed", seed, *flags,
+                         *tokens)
+            assert [int(v) for v in out.split()] == fx[f"{case}_s{j}_{tag}"].tolist(), f"{case} setting {j} {tag}"
+
+
+def test_cli_eos_ctx_and_expert_cache_line(tmp_path):
+    spec, cfg, path = write_case("ref_bf16", tmp_path)
+    fx = np.load(os.path.join(GOLDEN, "ref_bf16.npz"))
+    tokens = [int(t) for t in fx["tokens"]]
+    full = fx["gen_scalar"].tolist()
+    eos = full[2]
+    out, _ = run(path, "--gen", spec["n_gen"], "--eos", eos, *tokens)
+    assert [int(v) for v in out.split()] == full[:full.index(eos) + 1]  # eos printed, then stop
+    out, _ = run(path, "--gen", 50, "--ctx", len(tokens) + 3, *tokens)  # clamped to ctx - prompt
+    assert [int(v) for v in out.split()] == full[:3]
+    # --dump and --gen together: both outputs as separate runs give them
+    lp, rp = tmp_path / "l.bin", tmp_path / "r.bin"
+    out, err = run(path, "--dump", lp, rp, "--gen", spec["n_gen"], "--expert-cache-mib", 64, *tokens)
+    assert [int(v) for v in out.split()] == full
+    assert np.array_equal(np.fromfile(rp, dtype="<i4").reshape(fx["routing_scalar"].shape), fx["routing_scalar"])
+    stats = {k: int(v) for k, v in re.findall(r"(hits|misses|evictions|bytes_read|resident_bytes|capacity_bytes)=(\d+)",
+                                              err)}
+    stride = po.layout(cfg)["expert_stride"]
+    assert stats["misses"] == cfg.n_layers * cfg.n_experts and stats["evictions"] == 0
+    assert stats["bytes_read"] == stats["misses"] * stride
+    assert stats["hits"] > 0
+    out, err = run(path, "--gen", 2, "--kernel", "hip", *tokens)
+    assert "matvec kernel: hip-gfx950" in err and len(out.split()) == 2
