@@ -191,13 +191,19 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
 
 /* ---- instrumentation (the reference's only timing is its stderr tok/s line, rabbit2.c:742-744) ----
  * While enabled, every kernel launch of rbt_hip_moe_dev is bracketed by HIP events on the handle
- * stream and its duration is accumulated under its name ("router", "topk", "gateup",
+ * stream and its duration is counted under its name ("router", "topk", "gateup",
  * "down_combine"; the grouped path adds "dispatch" -- the activation hi/lo split and the per-expert
  * lists -- and "combine", and its "down_combine" is the down GEMM alone); rbt_hip_forward adds
- * "embed", "attn_norm", "qkv" (RMSNorm + q/k/v), "attention", "attn_merge", "wo", "ffn_norm", "lm_head" (final
- * norm + lm_head, with the argmax inside where the rows allow) and "argmax" (otherwise). Each timed launch then waits for its own work (rbt_hip_generate
- * is never timed this way). rbt_hip_profile_get returns 0 for an unknown name. Meant for
- * measurement passes, not for the timed hot loop. */
+ * "embed", "attn_norm", "qkv" (RMSNorm + q/k/v), "attention", "attn_merge", "wo", "ffn_norm",
+ * "lm_head" (final norm + lm_head, with the argmax inside where the rows allow) and "argmax"
+ * (otherwise). rbt_hip_generate is never timed this way. Modes (on):
+ *   0  off.
+ *   1  each call waits for its own kernels and adds their durations (eager calls only).
+ *   2  deferred: each launch takes a fresh event pair and nothing waits, so timed calls run back
+ *      to back as in a decode loop; rbt_hip_profile_get waits for the stream and returns the
+ *      durations of every launch since the mode was set (at most 4096 per name are timed).
+ * Setting a mode clears the counts; neither mode is for stream capture (HIP graphs do not time
+ * events). rbt_hip_profile_get fails for an unknown name. */
 int rbt_hip_profile_enable(rbt_hip *h, int on);
 int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches);
 

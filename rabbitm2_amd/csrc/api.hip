@@ -41,12 +41,19 @@ const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_co
                                             "embed", "attn_norm", "qkv", "attention", "attn_merge", "wo", "ffn_norm",
                                             "lm_head", "argmax"};
 
+// mode 1: one event pair per kernel kind, read after every call (each call waits for its work).
+// mode 2 (deferred): every launch takes a fresh pair from a per-kind pool and nothing waits, so the
+// timed calls run back to back as in a decode loop; rbt_hip_profile_get reads every pair taken since
+// the mode was set. (HIP graphs do not time events, so neither mode is meant for stream capture.)
+constexpr size_t kProfPoolMax = 4096;  // pairs per kind in mode 2
 struct Profile {
-    bool on = false;
+    int mode = 0;
     hipEvent_t ev[kProfCount][2] = {};
     bool used[kProfCount] = {};
     double total_ms[kProfCount] = {};
     uint64_t launches[kProfCount] = {};
+    std::vector<hipEvent_t> pool[kProfCount];  // mode 2: pairs (2i, 2i + 1)
+    size_t next[kProfCount] = {};
 };
 
 // Decode state of the full forward pass (rbt_hip_state_init): one allocation carved into the KV cache
@@ -248,17 +255,28 @@ int stage_reserve(rbt_hip *h, uint64_t bytes) {
 Launch lc(rbt_hip *h, int k) {
     Launch L;
     L.s = h->stream;
-    if (h->prof.on && k >= 0) {
-        L.start = h->prof.ev[k][0];
-        L.stop = h->prof.ev[k][1];
-        h->prof.used[k] = true;
+    Profile &P = h->prof;
+    if (P.mode == 1 && k >= 0) {
+        L.start = P.ev[k][0];
+        L.stop = P.ev[k][1];
+        P.used[k] = true;
+    } else if (P.mode == 2 && k >= 0 && P.next[k] < kProfPoolMax) {
+        std::vector<hipEvent_t> &pool = P.pool[k];
+        while (pool.size() < 2 * (P.next[k] + 1)) {
+            hipEvent_t ev = nullptr;
+            if (hipEventCreate(&ev) != hipSuccess) return L;  // out of events: this launch goes untimed
+            pool.push_back(ev);
+        }
+        L.start = pool[2 * P.next[k]];
+        L.stop = pool[2 * P.next[k] + 1];
+        P.next[k]++;
     }
     return L;
 }
 
-// Waits for the call's events and adds each bracketed kernel's duration.
+// Mode 1: waits for the call's events and adds each bracketed kernel's duration.
 int prof_collect(rbt_hip *h) {
-    if (!h->prof.on) return 1;
+    if (h->prof.mode != 1) return 1;
     for (int k = 0; k < kProfCount; k++) {
         if (!h->prof.used[k]) continue;
         HIP_OK(h, hipEventSynchronize(h->prof.ev[k][1]));
@@ -476,9 +494,11 @@ void rbt_hip_free(rbt_hip *h) {
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     ws_release(h->ws);
     (void)hipFree(h->ds.block);
-    for (int k = 0; k < kProfCount; k++)
+    for (int k = 0; k < kProfCount; k++) {
         for (int j = 0; j < 2; j++)
             if (h->prof.ev[k][j]) (void)hipEventDestroy(h->prof.ev[k][j]);
+        for (hipEvent_t ev : h->prof.pool[k]) (void)hipEventDestroy(ev);
+    }
     (void)hipFree(h->stage);
     (void)hipFree(h->model);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -869,7 +889,8 @@ void *rbt_hip_stream(rbt_hip *h) { return h ? static_cast<void *>(h->stream) : n
 int rbt_hip_profile_enable(rbt_hip *h, int on) {
     if (!h) return fail(nullptr, "profile: handle is NULL");
     if (!set_device(h)) return 0;
-    if (on && !h->prof.ev[0][0]) {
+    if (on < 0 || on > 2) return fail(h, "profile: mode must be 0, 1 or 2");
+    if (on == 1 && !h->prof.ev[0][0]) {
         for (int k = 0; k < kProfCount; k++)
             for (int j = 0; j < 2; j++) HIP_OK(h, hipEventCreate(&h->prof.ev[k][j]));
     }
@@ -878,20 +899,33 @@ int rbt_hip_profile_enable(rbt_hip *h, int on) {
             h->prof.total_ms[k] = 0.0;
             h->prof.launches[k] = 0;
             h->prof.used[k] = false;
+            h->prof.next[k] = 0;
         }
     }
-    h->prof.on = on != 0;
+    h->prof.mode = on;
     return 1;
 }
 
 int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches) {
     if (!h || !kernel) return fail(h, "profile_get: NULL argument");
     for (int k = 0; k < kProfCount; k++) {
-        if (strcmp(kernel, kProfNames[k]) == 0) {
-            if (total_ms) *total_ms = h->prof.total_ms[k];
-            if (launches) *launches = h->prof.launches[k];
+        if (strcmp(kernel, kProfNames[k]) != 0) continue;
+        if (h->prof.mode == 2) {  // every pair taken since the mode was set
+            if (!set_device(h)) return 0;
+            HIP_OK(h, hipStreamSynchronize(h->stream));
+            double tot = 0.0;
+            for (size_t i = 0; i < h->prof.next[k]; i++) {
+                float ms = 0.0f;
+                HIP_OK(h, hipEventElapsedTime(&ms, h->prof.pool[k][2 * i], h->prof.pool[k][2 * i + 1]));
+                tot += ms;
+            }
+            if (total_ms) *total_ms = tot;
+            if (launches) *launches = h->prof.next[k];
             return 1;
         }
+        if (total_ms) *total_ms = h->prof.total_ms[k];
+        if (launches) *launches = h->prof.launches[k];
+        return 1;
     }
     return fail(h, "profile_get: unknown kernel name '%s'", kernel);
 }
@@ -1034,12 +1068,12 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
     const StepState st{0, n_prompt, 0, 0, h->seed ? h->seed : 0x9E3779B97F4A7C15ull, 0};  // rabbit2.c:723
     HIP_OK(h, hipMemcpyAsync(h->ds.seq, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
-    const bool prof = h->prof.on;
-    h->prof.on = false;
+    const int prof = h->prof.mode;
+    h->prof.mode = 0;
     hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     int ok = capture_step(h, false, &g_adv) && capture_step(h, true, &g_fin);
-    h->prof.on = prof;
+    h->prof.mode = prof;
     auto cleanup = [&]() {
         if (g_adv) (void)hipGraphExecDestroy(g_adv);
         if (g_fin) (void)hipGraphExecDestroy(g_fin);
@@ -1133,12 +1167,12 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
         HIP_OK(h, hipMemcpyAsync(h->ds.seq + (size_t)b * ctx, prompts + (size_t)b * n_prompt, 4 * (size_t)n_prompt,
                                  hipMemcpyHostToDevice, h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, st.data(), sizeof(StepState) * B, hipMemcpyHostToDevice, h->stream));
-    const bool prof = h->prof.on;
-    h->prof.on = false;
+    const int prof = h->prof.mode;
+    h->prof.mode = 0;
     hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     int ok = capture_step(h, false, &g_adv) && capture_step(h, true, &g_fin);
-    h->prof.on = prof;
+    h->prof.mode = prof;
     hipError_t e = hipSuccess;
     if (ok) {
         for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);

@@ -191,7 +191,8 @@ class Device:
                                                offset))
 
     def profile(self, on):
-        self._check(self.L.rbt_hip_profile_enable(self.h, 1 if on else 0))
+        """on: False/0 off, True/1 per call (each call waits), 2 deferred (nothing waits)."""
+        self._check(self.L.rbt_hip_profile_enable(self.h, int(on)))
 
     def profile_get(self, kernel):
         ms, n = C.c_double(), C.c_uint64()

@@ -129,6 +129,33 @@ def test_olmoe_decode_fused_and_four_launch_paths(dev, olmoe_layer):
         dev.set_option("fused_decode", 1)
 
 
+def test_profile_deferred_mode(dev, olmoe_layer):
+    """Profiling mode 2 times every launch without waiting between calls: profile_get reports each
+    kernel of every call since the mode was set, and the outputs are unchanged."""
+    dev.set_router_order(po.ORDER_AVX2)
+    L = olmoe_layer.desc()
+    dev.reserve(L, 1)
+    xb = dev.upload_array(olmoe_layer.make_x(1, seed=9))
+    moe = dev.malloc(2048 * 4)
+    try:
+        dev.moe_dev(L, xb, 1, moe=moe)
+        dev.synchronize()
+        want = dev.d2h(moe, (2048,), np.float32)
+        dev.profile(2)
+        for _ in range(5):
+            dev.moe_dev(L, xb, 1, moe=moe)
+        for name in ("router", "gateup", "down_combine"):
+            tot, n = dev.profile_get(name)
+            assert n == 5 and 0 < 1000.0 * tot / n < 1000.0, (name, tot, n)
+        assert dev.d2h(moe, (2048,), np.float32).tobytes() == want.tobytes()
+        dev.profile(2)  # setting the mode again clears the counts
+        assert dev.profile_get("gateup")[1] == 0
+    finally:
+        dev.profile(0)
+        dev.free(xb)
+        dev.free(moe)
+
+
 def test_olmoe_decode_deterministic(dev, olmoe_layer):
     dev.set_router_order(po.ORDER_AVX2)
     xb = olmoe_layer.make_x(1, seed=7)
