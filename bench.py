@@ -491,6 +491,7 @@ def cpu_full_model(dev, cfg, prompt, seconds):
 PREFILL_T = 512
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak, published
 PREFILL_KERNELS = ("router", "topk", "dispatch", "gateup", "down_combine", "combine")
+PREFILL_GRAPH_CALLS = 8  # calls per captured graph in the prefill leg
 
 
 def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
@@ -528,12 +529,14 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             dev.moe_dev(L, xb, T, moe=moe)
         hipapi.hipEventRecord(e1, stream)
         us_eager = 1000.0 * elapsed(e0, e1) / reps
-        # the same call captured as a HIP graph (kernels only), checked against the eager output
+        # the same call captured PREFILL_GRAPH_CALLS times into a HIP graph (kernels only), checked
+        # against the eager output; one graph launch per PREFILL_GRAPH_CALLS calls
         dev.synchronize()
         eager_out = dev.d2h(moe, (T, D), np.float32)
         graph, gexec = C.c_void_p(), C.c_void_p()
         assert hipapi.hipStreamBeginCapture(stream, 2) == 0
-        dev.moe_dev(L, xb, T, moe=moe)
+        for _ in range(PREFILL_GRAPH_CALLS):
+            dev.moe_dev(L, xb, T, moe=moe)
         assert hipapi.hipStreamEndCapture(stream, C.byref(graph)) == 0
         assert hipapi.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0) == 0
         for _ in range(3):
@@ -541,14 +544,15 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             assert hipapi.hipGraphLaunch(gexec, stream) == 0
             dev.synchronize()
             assert dev.d2h(moe, (T, D), np.float32).tobytes() == eager_out.tobytes(), "prefill graph replay differs"
+        greps = max(1, reps // PREFILL_GRAPH_CALLS)
         hipapi.hipEventRecord(e0, stream)
-        for _ in range(reps):
+        for _ in range(greps):
             hipapi.hipGraphLaunch(gexec, stream)
         hipapi.hipEventRecord(e1, stream)
-        us = 1000.0 * elapsed(e0, e1) / reps
+        us = 1000.0 * elapsed(e0, e1) / (greps * PREFILL_GRAPH_CALLS)
         hipapi.hipGraphExecDestroy(gexec)
         hipapi.hipGraphDestroy(graph)
-        dev.profile(True)
+        dev.profile(2)  # per-kernel events, calls back to back
         for _ in range(reps):
             dev.moe_dev(L, xb, T, moe=moe)
         kern = {}
@@ -556,14 +560,16 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             tot, n = dev.profile_get(kname)
             if n:
                 kern[kname] = {"avg_us": round(1000.0 * tot / n, 2)}
-        dev.profile(False)
+        dev.profile(0)
         counts = dev.expert_counts(E)
-        tiles = int(sum((c + 63) // 64 for c in counts))
+        tiles = int(sum((c + 63) // 64 for c in counts))  # the GEMMs' 64-row tiles
+        issued_rows = int(sum((c + 15) // 16 * 16 for c in counts))
         for kname, fl in gemm_flops.items():
             if kname in kern:
                 t = kern[kname]["avg_us"] * 1e-6
-                # issued: every 64-row tile runs in full, and each product is two bf16 MFMAs (hi + lo part)
-                issued = 2 * fl * (tiles * 64) / P
+                # issued: the MFMAs run per block of 16 list rows (a block past an expert's list is
+                # skipped, a partly filled one runs in full), two bf16 MFMAs per product (hi + lo part)
+                issued = 2 * fl * issued_rows / P
                 kern[kname]["mfma_util_alg"] = round(fl / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
                 kern[kname]["mfma_util_issued"] = round(issued / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
                 wbytes = E * (2 if kname == "gateup" else 1) * H * D * esz
@@ -580,8 +586,8 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             "row_tiles": tiles,
         }
     out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,
-           "note": "per-call time of the whole MoE block (router .. combine), HIP graph replay of one call "
-                   "(us_per_call_eager: back-to-back eager launches), inputs in HBM",
+           "note": f"per-call time of the whole MoE block (router .. combine), HIP graph of {PREFILL_GRAPH_CALLS} "
+                   "calls replayed (us_per_call_eager: back-to-back eager calls), inputs in HBM",
            **res}
     if with_cpu:
         out["cpu_baseline"] = cpu_prefill(dev, routers, experts, stride, xs, 64)
