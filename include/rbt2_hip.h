@@ -65,6 +65,10 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *   "fused_decode"        1 (default): a batch-1 block of up to 64 experts runs the softmax + top-k
  *                         inside the expert gate/up kernel (router logits, gate/up, down: three
  *                         launches); 0: a separate top-k launch (four launches). Same results.
+ *   "batch_mfma"          1 (default): the batched forward (rbt_hip_batch_init with n_seq > 1) runs
+ *                         q/k/v, wo and lm_head for up to 64 sequences on the matrix cores (bf16
+ *                         weights; activations as bf16 hi + lo parts, exact products); 0: VALU dot
+ *                         products. Both agree with the engine to rounding.
  *   "prefill_min_tokens"  smallest T (1..65536, default 12) that takes the grouped path for bf16
  *                         weights: (token, slot) pairs dispatched into per-expert lists and the
  *                         expert FFN run as grouped GEMMs on the matrix cores, each expert's weights

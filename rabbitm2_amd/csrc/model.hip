@@ -328,6 +328,100 @@ __global__ __launch_bounds__(256) void dense_batch_kernel(const float *__restric
     }
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// out[b][r] = W[r] . x[b] for B <= 16 * TB token rows on the matrix cores (batched decode: q/k/v, wo,
+// lm_head): one block per 16 weight rows (one segment); its NW waves split the row into NW slices of
+// WS k-steps of 32. A operand: 16 weight rows x 32 of K, bf16 straight from the weights (exact); B
+// operand: the tokens' bf16 hi and lo planes (hi + lo = x to ~16 bits, each product with a bf16 weight
+// exact in the f32 accumulator). A wave issues all of its weight loads and then, per pair of 16-token
+// blocks, all of their activation loads before the first MFMA, so a block costs about one memory round
+// trip. v_mfma_f32_16x16x32_bf16 per (k-step, 16 tokens, part); the NW slices are added in order
+// through LDS. Lane l of a 16 x 16 result holds rows 4 (l / 16) + v, token l % 16.
+// MODE 0: segment outputs; 1: resid[b][r] += (one segment).
+template <int KS>
+struct MfmaShape {
+    static constexpr int NW = KS >= 4 ? 16 : 4 * KS;  // waves per block
+    static constexpr int WS = 4 * KS / NW;             // k-steps per wave (1..4)
+};
+template <int KS, int TB, int MODE>
+__global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__restrict__ x_hi,
+                                                          const uint16_t *__restrict__ x_lo, int xs, int B, Segs sg,
+                                                          int total_rows, float *__restrict__ resid) {
+    constexpr int K = 128 * KS, NW = MfmaShape<KS>::NW, WS = MfmaShape<KS>::WS;
+    static_assert(WS >= 1 && WS <= 4 && NW * WS * 32 == K, "k split");
+    __shared__ f32x4 part[NW][TB][kWave];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row0 = blockIdx.x * 16;
+    int s = 0, r = row0;  // the tile's segment and first row in it (segments are whole tiles)
+    while (s < 2 && r >= sg.rows[s]) {
+        r -= sg.rows[s];
+        ++s;
+    }
+    const size_t koff = (size_t)w * WS * 32 + 8 * (lane >> 4);
+    const uint8_t *wp = sg.W[s] + ((size_t)(r + (lane & 15)) * K + koff) * 2;
+    u32x4 a[WS];
+#pragma unroll
+    for (int i = 0; i < WS; ++i) a[i] = ld_stream_u4(wp + 64 * i);
+    f32x4 acc[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int tb0 = 0; tb0 < TB; tb0 += 2) {
+        constexpr int NBMAX = TB < 2 ? TB : 2;
+        u32x4 bh[WS][NBMAX], bl[WS][NBMAX];
+#pragma unroll
+        for (int j = 0; j < NBMAX; ++j) {
+            if (tb0 + j < TB) {
+                const size_t t = (size_t)min(16 * (tb0 + j) + (lane & 15), B - 1);
+#pragma unroll
+                for (int i = 0; i < WS; ++i) {
+                    bh[i][j] = *reinterpret_cast<const u32x4 *>(x_hi + t * xs + koff + 32 * i);
+                    bl[i][j] = *reinterpret_cast<const u32x4 *>(x_lo + t * xs + koff + 32 * i);
+                }
+            }
+        }
+        // every load out before the first MFMA (the scheduler would otherwise reuse registers and
+        // serialise round trips)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < WS; ++i) {
+            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a[i]);
+#pragma unroll
+            for (int j = 0; j < NBMAX; ++j) {
+                if (tb0 + j < TB) {
+                    acc[tb0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        av, __builtin_bit_cast(bf16x8_t, bh[i][j]), acc[tb0 + j], 0, 0, 0);
+                    acc[tb0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        av, __builtin_bit_cast(bf16x8_t, bl[i][j]), acc[tb0 + j], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) part[w][tb][lane] = acc[tb];
+    __syncthreads();
+    // one output element per thread: (block tb, lane l, element j) summed over the NW slices in order
+    const float *pf = reinterpret_cast<const float *>(part);
+    for (int e = threadIdx.x; e < TB * kWave * 4; e += blockDim.x) {
+        float v[NW];
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) v[ww] = pf[(size_t)ww * TB * kWave * 4 + e];
+        float sum = v[0];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) sum = sum + v[ww];
+        const int tb = e / (kWave * 4), l = (e / 4) % kWave, j = e % 4;
+        const int t = 16 * tb + (l & 15), rr = 4 * (l >> 4) + j;
+        if (t >= B) continue;
+        if constexpr (MODE == 1) {
+            float *dst = resid + (size_t)t * total_rows + row0 + rr;
+            *dst = *dst + sum;
+        } else {
+            sg.out[s][(size_t)t * sg.rows[s] + r + rr] = sum;
+        }
+    }
+}
+
 // Greedy argmax over the lm_head blocks' candidates (value, first index; index -1 = none), then the step
 // advances like argmax_kernel: the engine's scan keeps index 0 when logits[0] is NaN or nothing beats it.
 __global__ __launch_bounds__(1024) void argmax_cand_kernel(const float2 *__restrict__ cand, int nc,
@@ -596,7 +690,8 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
 // attn_out[h*hd + i] = sum_s a_s o_s[i] / sum_s a_s l_s with a_s = exp(m_s - max m): block h merges the
 // S split partials of head h (the engine's softmax-weighted sum over all positions, rabbit2.c:493-498).
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part, int hd, int S,
-                                                         float *__restrict__ ao) {
+                                                         float *__restrict__ ao, uint16_t *__restrict__ ao_hi,
+                                                         uint16_t *__restrict__ ao_lo, int plane_stride) {
     __shared__ float wa[64], s_inv;
     const int h = blockIdx.x, b = blockIdx.y, n_heads = gridDim.x;
     const float *ph = part + ((size_t)b * n_heads + h) * S * (hd + 2);
@@ -627,7 +722,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
         for (int q = 0; q < 16; ++q)
             if (q < S) o += wa[q] * ov[q];
         for (int q = 16; q < S; ++q) o += wa[q] * ph[(size_t)q * (hd + 2) + 2 + i];
-        ao[(size_t)h * hd + i] = o * s_inv;
+        const float v = o * s_inv;
+        const size_t oi = (size_t)b * plane_stride + (size_t)h * hd + i;
+        ao[(size_t)h * hd + i] = v;
+        if (ao_hi) {
+            const uint32_t hb = f32_to_bf16_rne(v);
+            ao_hi[oi] = (uint16_t)hb;
+            ao_lo[oi] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(hb << 16));
+        }
     }
 }
 
@@ -649,10 +751,23 @@ __global__ __launch_bounds__(256) void wo_kernel(const float *__restrict__ ao, i
 
 // ---------------------------------------------------------------- RMSNorm (one block)
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w, int n,
-                                                       float eps, float *__restrict__ out) {
+                                                       float eps, float *__restrict__ out, uint16_t *__restrict__ hi,
+                                                       uint16_t *__restrict__ lo, int plane_stride) {
     __shared__ float red[16];
     x += (size_t)blockIdx.x * n;  // one row per block
     out += (size_t)blockIdx.x * n;
+    if (hi) {
+        hi += (size_t)blockIdx.x * plane_stride;
+        lo += (size_t)blockIdx.x * plane_stride;
+    }
+    auto put = [&](int i, float v) {
+        out[i] = v;
+        if (hi) {
+            const uint32_t h = f32_to_bf16_rne(v);
+            hi[i] = (uint16_t)h;
+            lo[i] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(h << 16));
+        }
+    };
     // rows of up to 4 * 1024 elements from registers (x and w loaded together), longer ones by the loop
     constexpr int U = 4;
     float xr[U], wr[U];
@@ -672,9 +787,9 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int i = threadIdx.x + 1024 * u;
-        if (i < n) out[i] = xr[u] * inv * wr[u];
+        if (i < n) put(i, xr[u] * inv * wr[u]);
     }
-    for (int i = threadIdx.x + 1024 * U; i < n; i += blockDim.x) out[i] = x[i] * inv * w[i];
+    for (int i = threadIdx.x + 1024 * U; i < n; i += blockDim.x) put(i, x[i] * inv * w[i]);
 }
 
 // ---------------------------------------------------------------- greedy argmax (rabbit2.c:552-556)
@@ -993,6 +1108,60 @@ hipError_t dense_batch_dt(const Launch &L, int D, const float *xin, int B, const
     }
 }
 
+bool dense_mfma_supported(int dtype, int B, int K, const void *const W[3], const int rows[3]) {
+    if (dtype != RBT_DT_BF16 || B < 1 || B > 64 || K % 128 != 0) return false;
+    const int ks = K / 128;
+    if (ks != 1 && ks != 2 && ks != 4 && ks != 8 && ks != 16) return false;
+    for (int i = 0; i < 3; ++i)
+        if (rows[i] % 16 != 0 || (rows[i] && (reinterpret_cast<uintptr_t>(W[i]) & 15u))) return false;
+    return true;
+}
+
+namespace {
+template <int KS, int MODE>
+hipError_t dense_mfma_ks(const Launch &L, const uint16_t *xh, const uint16_t *xl, int xs, int B, const Segs &sg,
+                         int total, float *resid) {
+    const dim3 g((unsigned)(total / 16)), b(64 * MfmaShape<KS>::NW);
+    switch ((B + 15) / 16) {
+        case 1: return launch(L, dense_mfma_kernel<KS, 1, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
+        case 2: return launch(L, dense_mfma_kernel<KS, 2, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
+        case 3: return launch(L, dense_mfma_kernel<KS, 3, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
+        case 4: return launch(L, dense_mfma_kernel<KS, 4, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
+        default: return hipErrorNotSupported;
+    }
+}
+template <int MODE>
+hipError_t dense_mfma_mode(const Launch &L, const uint16_t *xh, const uint16_t *xl, int xs, int B, int K,
+                           const Segs &sg, int total, float *resid) {
+    switch (K / 128) {
+        case 1: return dense_mfma_ks<1, MODE>(L, xh, xl, xs, B, sg, total, resid);
+        case 2: return dense_mfma_ks<2, MODE>(L, xh, xl, xs, B, sg, total, resid);
+        case 4: return dense_mfma_ks<4, MODE>(L, xh, xl, xs, B, sg, total, resid);
+        case 8: return dense_mfma_ks<8, MODE>(L, xh, xl, xs, B, sg, total, resid);
+        case 16: return dense_mfma_ks<16, MODE>(L, xh, xl, xs, B, sg, total, resid);
+        default: return hipErrorNotSupported;
+    }
+}
+}  // namespace
+
+hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16_t *x_lo, int x_stride, int B,
+                             int K, const void *const W[3], float *const out[3], const int rows[3], float *resid) {
+    Segs sg;
+    int total = 0;
+    for (int i = 0; i < 3; ++i) {
+        sg.W[i] = static_cast<const uint8_t *>(W[i]);
+        sg.out[i] = out[i];
+        sg.rows[i] = rows[i];
+        total += rows[i];
+    }
+    if (total == 0 || B == 0) return hipSuccess;
+    if (!dense_mfma_supported(RBT_DT_BF16, B, K, W, rows) || (resid && rows[1] + rows[2] != 0))
+        return hipErrorNotSupported;
+    if (x_stride < K || x_stride % 8 != 0) return hipErrorInvalidValue;
+    return resid ? dense_mfma_mode<1>(L, x_hi, x_lo, x_stride, B, K, sg, total, resid)
+                 : dense_mfma_mode<0>(L, x_hi, x_lo, x_stride, B, K, sg, total, nullptr);
+}
+
 hipError_t launch_dense_batch(const Launch &L, int dtype, const float *xin, int B, int D, const void *const W[3],
                               float *const out[3], const int rows[3], float *resid) {
     Segs sg;
@@ -1095,8 +1264,11 @@ hipError_t launch_attention(const Launch &L, const float *q, const float *k, con
                   seq_stride, rope_cs, part);
 }
 
-hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B) {
-    return launch(L, attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)B), dim3(256), 0, part, hd, S, ao);
+hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,
+                             uint16_t *ao_hi, uint16_t *ao_lo, int plane_stride) {
+    if ((ao_hi == nullptr) != (ao_lo == nullptr) || (ao_hi && plane_stride < n_heads * hd)) return hipErrorInvalidValue;
+    return launch(L, attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)B), dim3(256), 0, part, hd, S, ao, ao_hi,
+                  ao_lo, plane_stride);
 }
 
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x) {
@@ -1111,8 +1283,11 @@ hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, con
                : launch(L, wo_kernel<RBT_DT_F32, false>, g, b, lds, ao, q_dim, W, D, x);
 }
 
-hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B) {
-    return launch(L, rmsnorm_kernel, dim3((unsigned)B), dim3(1024), 0, x, w, n, eps, out);
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B,
+                          uint16_t *out_hi, uint16_t *out_lo, int plane_stride) {
+    if ((out_hi == nullptr) != (out_lo == nullptr) || (out_hi && plane_stride < n)) return hipErrorInvalidValue;
+    return launch(L, rmsnorm_kernel, dim3((unsigned)B), dim3(1024), 0, x, w, n, eps, out, out_hi, out_lo,
+                  plane_stride);
 }
 
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B) {

@@ -35,11 +35,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kMT = 64;  // rows (pairs) per tile
 constexpr int kDispatchMaxE = 256;
 
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
-}
 
 // ---------------------------------------------------------------- dispatch (one block, 1024 threads)
 // routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);

@@ -15,6 +15,15 @@ constexpr int kWave = 64;  // CDNA wavefront width
 __device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xFFFF0000u); }
 
+// f32 -> bf16 bits, round to nearest even (the converter's rule, rabbit2/ref/rbt2.py:106-113, finite
+// values). Activations multiplied on the matrix cores are split into hi = bf16(x) and
+// lo = bf16(x - hi), which carry ~16 significant bits; products with exact bf16 weights are exact.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
 template <int DT>
 __device__ __forceinline__ float load_w(const void *W, size_t i) {
     if constexpr (DT == RBT_DT_F32) {
@@ -199,13 +208,27 @@ hipError_t launch_attention(const Launch &L, const float *q, const float *k, con
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
                             float *part, int B);
-hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B);
+hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,
+                             uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr, int plane_stride = 0);
 // Dense rows over B token vectors xin [B][D] (batched decode): out_s [B][rows_s], or with resid != NULL
 // resid [B][rows] += (one segment). Same row shapes as dense_supported.
 hipError_t launch_dense_batch(const Launch &L, int dtype, const float *xin, int B, int D, const void *const W[3],
                               float *const out[3], const int rows[3], float *resid);
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x);
-hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B);
+// out_hi / out_lo (may be null): the rows' bf16 hi and lo parts as well (launch_dense_mfma's input), rows
+// plane_stride elements apart.
+hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B,
+                          uint16_t *out_hi = nullptr, uint16_t *out_lo = nullptr, int plane_stride = 0);
+// launch_dense_batch on the matrix cores: B <= 64 token rows given as bf16 hi/lo planes [B][K]; bf16
+// weights only, K = 128 * {1, 2, 4, 8, 16}, every segment a multiple of 16 rows
+// (dense_mfma_supported). The products are exact; the sums run in the MFMA order, then the slices of
+// K in a fixed order.
+bool dense_mfma_supported(int dtype, int B, int K, const void *const W[3], const int rows[3]);
+hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16_t *x_lo, int x_stride, int B,
+                             int K, const void *const W[3], float *const out[3], const int rows[3], float *resid);
+// Row stride of the hi/lo planes for rows of n elements: 128 bytes more than a multiple of 4 KiB, so the
+// rows that one load instruction touches fall on different L2 channels.
+inline int mfma_plane_stride(int n) { return (n + 2047) / 2048 * 2048 + 64; }
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B);
 hipError_t launch_advance(const Launch &L, StepState *st, int B);
 

@@ -60,6 +60,36 @@ def test_forward_batch_matches_each_sequence_alone(dev, case, B, n):
             assert err <= LOGIT_RTOL, f"{case} seq {b} pos {p}: logits error {err:.2e}"
 
 
+@pytest.mark.parametrize("B", [33, 64])
+def test_batch_matrix_core_matvecs_agree_with_vector_ones(dev, B):
+    """The batched q/k/v, wo and lm_head on the matrix cores (option batch_mfma, the default; B = 33 fills
+    a last block of 16 tokens with one sequence) against the VALU dot products: routing identical,
+    logits within rounding of each other, and the first and last sequences against the oracle."""
+    spec, cfg, model = build("olmoe_layer_bf16")
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, 2, seed=B + 100)
+    runs = {}
+    try:
+        for mode in (1, 0):
+            dev.set_option("batch_mfma", mode)
+            dev.batch_init(B, 0)
+            runs[mode] = [dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
+                                            cfg.top_k) for p in range(2)]
+    finally:
+        dev.set_option("batch_mfma", 1)
+    for p in range(2):
+        (lm, rm), (lv, rv) = runs[1][p], runs[0][p]
+        assert np.array_equal(rm, rv)
+        for b in range(B):
+            assert normwise_err(lm[b], lv[b]) <= 1e-4
+    for b in (0, B - 1):
+        wl, wr, _ = po.run(model, prompts[b], order=po.ORDER_AVX2)
+        for p in range(2):
+            assert np.array_equal(runs[1][p][1][:, b, :], wr[p])
+            assert normwise_err(runs[1][p][0][b], wl[p]) <= LOGIT_RTOL
+
+
 def test_forward_batch_sequences_restart_independently(dev):
     """Sequence 1 starts over at position 0 every 3 steps while sequence 0 runs on: each is its own
     forward() stream (a restart overwrites only that sequence's cache)."""
