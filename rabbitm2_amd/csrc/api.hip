@@ -65,7 +65,7 @@ struct DecodeState {
     float *kc = nullptr, *vc = nullptr;  // [n_seq][n_layers][ctx][kv_dim]
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr;
     float *part = nullptr;        // attention split partials [n_heads][S][hd + 2]
-    uint16_t *xh = nullptr, *xl = nullptr;  // bf16 hi/lo planes [n_seq][max(dim, q_dim)] for the MFMA matvecs
+    uint16_t *xh = nullptr, *xl = nullptr;  // bf16 hi/lo matrix-core planes of n_seq rows of max(dim, q_dim)
     float2 *rope_cs = nullptr;    // [ctx][hd/2] (cos, sin) of the RoPE angles
     float2 *cand = nullptr;       // lm_head blocks' argmax candidates
     float *sprob = nullptr;       // sampler scratch [n_seq][vocab]
@@ -343,7 +343,6 @@ int enqueue_step(rbt_hip *h, bool final) {
     DecodeState &ds = h->ds;
     const int B = ds.n_seq;
     const int D = c.dim, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
-    const int ps = mfma_plane_stride(D > qd ? D : qd);  // row stride of the hi/lo planes
     // with profiling on (eager calls only), every launch is timed by its own event pair and collected
     // right away, since each kernel kind runs once per layer
 #define STEP_LAUNCH(k, call)                  \
@@ -364,8 +363,8 @@ int enqueue_step(rbt_hip *h, bool final) {
             STEP_LAUNCH(kProfQkv, launch_dense_norm(L, c.dtype, ds.x, attn_norm, c.rms_eps, D, W, out, rows));
         } else if (dense && h->batch_mfma && dense_mfma_supported(c.dtype, B, D, W, rows)) {
             // batched on the matrix cores: the norm also writes the bf16 hi/lo planes of xb
-            STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl, ps));
-            STEP_LAUNCH(kProfQkv, launch_dense_mfma(L, ds.xh, ds.xl, ps, B, D, W, out, rows, nullptr));
+            STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl));
+            STEP_LAUNCH(kProfQkv, launch_dense_mfma(L, ds.xh, ds.xl, B, D, W, out, rows, nullptr));
         } else if (dense) {  // batched: the norm once per token, then every weight read once for all tokens
             STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B));
             STEP_LAUNCH(kProfQkv, launch_dense_batch(L, c.dtype, ds.xb, B, D, W, out, rows, nullptr));
@@ -388,9 +387,9 @@ int enqueue_step(rbt_hip *h, bool final) {
         const int wo_rows[3] = {D, 0, 0};
         const bool wo_mfma = B > 1 && h->batch_mfma && dense_mfma_supported(c.dtype, B, qd, Wo, wo_rows);
         STEP_LAUNCH(kProfAttnMerge, launch_attn_merge(L, ds.part, c.n_heads, hd, ds.S, ds.ao, B,
-                                                      wo_mfma ? ds.xh : nullptr, wo_mfma ? ds.xl : nullptr, ps));
+                                                      wo_mfma ? ds.xh : nullptr, wo_mfma ? ds.xl : nullptr));
         if (wo_mfma) {
-            STEP_LAUNCH(kProfWo, launch_dense_mfma(L, ds.xh, ds.xl, ps, B, qd, Wo, no_out, wo_rows, ds.x));
+            STEP_LAUNCH(kProfWo, launch_dense_mfma(L, ds.xh, ds.xl, B, qd, Wo, no_out, wo_rows, ds.x));
         } else if (dense_supported(c.dtype, qd, Wo, wo_rows)) {
             if (B == 1)
                 STEP_LAUNCH(kProfWo, launch_dense_resid(L, c.dtype, ds.ao, qd, h->model + ly.wo, D, ds.x));
@@ -436,8 +435,8 @@ int enqueue_step(rbt_hip *h, bool final) {
             if (dense && B == 1) {
                 STEP_LAUNCH(kProfLmHead, launch_dense_norm(L, c.dtype, ds.x, fn, c.rms_eps, D, W, out, rows));
             } else if (dense && h->batch_mfma && dense_mfma_supported(c.dtype, B, D, W, rows)) {
-                STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl, ps));
-                STEP_LAUNCH(kProfLmHead, launch_dense_mfma(L, ds.xh, ds.xl, ps, B, D, W, out, rows, nullptr));
+                STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl));
+                STEP_LAUNCH(kProfLmHead, launch_dense_mfma(L, ds.xh, ds.xl, B, D, W, out, rows, nullptr));
             } else if (dense) {
                 STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B));
                 STEP_LAUNCH(kProfLmHead, launch_dense_batch(L, c.dtype, ds.xb, B, D, W, out, rows, nullptr));
@@ -988,8 +987,8 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     const uint64_t o_x = carve(4 * B * D), o_xb = carve(4 * B * D), o_q = carve(4 * B * qd), o_k = carve(4 * B * kvd),
                    o_v = carve(4 * B * kvd), o_ao = carve(4 * B * qd);
     const uint64_t o_part = carve(4 * B * c.n_heads * ds.S * (hd + 2));
-    const uint64_t plane = (uint64_t)mfma_plane_stride((int)(D > qd ? D : qd));
-    const uint64_t o_xh = carve(2 * B * plane), o_xl = carve(2 * B * plane);
+    const uint64_t plane = B <= 64 ? (uint64_t)mfma_plane_elems((int)B, (int)(D > qd ? D : qd)) : 0;
+    const uint64_t o_xh = carve(2 * plane), o_xl = carve(2 * plane);
     const uint64_t o_rope = carve(8 * (uint64_t)ctx * (hd / 2));
     const uint64_t o_cand = carve(8 * (uint64_t)dense_argmax_blocks(c.vocab));
     const uint64_t o_sp = carve(4 * B * c.vocab), o_si = carve(4 * B * c.vocab);

@@ -334,7 +334,9 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // lm_head): one block per 16 weight rows (one segment); its NW waves split the row into NW slices of
 // WS k-steps of 32. A operand: 16 weight rows x 32 of K, bf16 straight from the weights (exact); B
 // operand: the tokens' bf16 hi and lo planes (hi + lo = x to ~16 bits, each product with a bf16 weight
-// exact in the f32 accumulator). A wave issues all of its weight loads and then, per pair of 16-token
+// exact in the f32 accumulator), as matrix-core planes (mfma_plane_index): each operand load of a wave
+// is one contiguous 1 KiB tile (at the lm_head shape 78 us, against 134 us for [B][K] rows, whose loads
+// touch 16 rows per instruction). A wave issues all of its weight loads and then, per pair of 16-token
 // blocks, all of their activation loads before the first MFMA, so a block costs about one memory round
 // trip. v_mfma_f32_16x16x32_bf16 per (k-step, 16 tokens, part); the NW slices are added in order
 // through LDS. Lane l of a 16 x 16 result holds rows 4 (l / 16) + v, token l % 16.
@@ -346,7 +348,7 @@ struct MfmaShape {
 };
 template <int KS, int TB, int MODE>
 __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__restrict__ x_hi,
-                                                          const uint16_t *__restrict__ x_lo, int xs, int B, Segs sg,
+                                                          const uint16_t *__restrict__ x_lo, int B, Segs sg,
                                                           int total_rows, float *__restrict__ resid) {
     constexpr int K = 128 * KS, NW = MfmaShape<KS>::NW, WS = MfmaShape<KS>::WS;
     static_assert(WS >= 1 && WS <= 4 && NW * WS * 32 == K, "k split");
@@ -373,11 +375,11 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
 #pragma unroll
         for (int j = 0; j < NBMAX; ++j) {
             if (tb0 + j < TB) {
-                const size_t t = (size_t)min(16 * (tb0 + j) + (lane & 15), B - 1);
 #pragma unroll
                 for (int i = 0; i < WS; ++i) {
-                    bh[i][j] = *reinterpret_cast<const u32x4 *>(x_hi + t * xs + koff + 32 * i);
-                    bl[i][j] = *reinterpret_cast<const u32x4 *>(x_lo + t * xs + koff + 32 * i);
+                    const size_t o = (((size_t)(w * WS + i) * TB + (tb0 + j)) * kWave + lane) * 8;
+                    bh[i][j] = *reinterpret_cast<const u32x4 *>(x_hi + o);
+                    bl[i][j] = *reinterpret_cast<const u32x4 *>(x_lo + o);
                 }
             }
         }
@@ -691,7 +693,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
 // S split partials of head h (the engine's softmax-weighted sum over all positions, rabbit2.c:493-498).
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part, int hd, int S,
                                                          float *__restrict__ ao, uint16_t *__restrict__ ao_hi,
-                                                         uint16_t *__restrict__ ao_lo, int plane_stride) {
+                                                         uint16_t *__restrict__ ao_lo) {
     __shared__ float wa[64], s_inv;
     const int h = blockIdx.x, b = blockIdx.y, n_heads = gridDim.x;
     const float *ph = part + ((size_t)b * n_heads + h) * S * (hd + 2);
@@ -723,7 +725,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
             if (q < S) o += wa[q] * ov[q];
         for (int q = 16; q < S; ++q) o += wa[q] * ph[(size_t)q * (hd + 2) + 2 + i];
         const float v = o * s_inv;
-        const size_t oi = (size_t)b * plane_stride + (size_t)h * hd + i;
+        const size_t oi = mfma_plane_index(b, h * hd + i, (gridDim.y + 15) / 16);
         ao[(size_t)h * hd + i] = v;
         if (ao_hi) {
             const uint32_t hb = f32_to_bf16_rne(v);
@@ -752,20 +754,18 @@ __global__ __launch_bounds__(256) void wo_kernel(const float *__restrict__ ao, i
 // ---------------------------------------------------------------- RMSNorm (one block)
 __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ w, int n,
                                                        float eps, float *__restrict__ out, uint16_t *__restrict__ hi,
-                                                       uint16_t *__restrict__ lo, int plane_stride) {
+                                                       uint16_t *__restrict__ lo) {
     __shared__ float red[16];
     x += (size_t)blockIdx.x * n;  // one row per block
     out += (size_t)blockIdx.x * n;
-    if (hi) {
-        hi += (size_t)blockIdx.x * plane_stride;
-        lo += (size_t)blockIdx.x * plane_stride;
-    }
+    const int tbs = (gridDim.x + 15) / 16;  // token blocks of the planes
     auto put = [&](int i, float v) {
         out[i] = v;
         if (hi) {
+            const size_t pi = mfma_plane_index(blockIdx.x, i, tbs);
             const uint32_t h = f32_to_bf16_rne(v);
-            hi[i] = (uint16_t)h;
-            lo[i] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(h << 16));
+            hi[pi] = (uint16_t)h;
+            lo[pi] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(h << 16));
         }
     };
     // rows of up to 4 * 1024 elements from registers (x and w loaded together), longer ones by the loop
@@ -1119,33 +1119,33 @@ bool dense_mfma_supported(int dtype, int B, int K, const void *const W[3], const
 
 namespace {
 template <int KS, int MODE>
-hipError_t dense_mfma_ks(const Launch &L, const uint16_t *xh, const uint16_t *xl, int xs, int B, const Segs &sg,
+hipError_t dense_mfma_ks(const Launch &L, const uint16_t *xh, const uint16_t *xl, int B, const Segs &sg,
                          int total, float *resid) {
     const dim3 g((unsigned)(total / 16)), b(64 * MfmaShape<KS>::NW);
     switch ((B + 15) / 16) {
-        case 1: return launch(L, dense_mfma_kernel<KS, 1, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
-        case 2: return launch(L, dense_mfma_kernel<KS, 2, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
-        case 3: return launch(L, dense_mfma_kernel<KS, 3, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
-        case 4: return launch(L, dense_mfma_kernel<KS, 4, MODE>, g, b, 0, xh, xl, xs, B, sg, total, resid);
+        case 1: return launch(L, dense_mfma_kernel<KS, 1, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
+        case 2: return launch(L, dense_mfma_kernel<KS, 2, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
+        case 3: return launch(L, dense_mfma_kernel<KS, 3, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
+        case 4: return launch(L, dense_mfma_kernel<KS, 4, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
         default: return hipErrorNotSupported;
     }
 }
 template <int MODE>
-hipError_t dense_mfma_mode(const Launch &L, const uint16_t *xh, const uint16_t *xl, int xs, int B, int K,
+hipError_t dense_mfma_mode(const Launch &L, const uint16_t *xh, const uint16_t *xl, int B, int K,
                            const Segs &sg, int total, float *resid) {
     switch (K / 128) {
-        case 1: return dense_mfma_ks<1, MODE>(L, xh, xl, xs, B, sg, total, resid);
-        case 2: return dense_mfma_ks<2, MODE>(L, xh, xl, xs, B, sg, total, resid);
-        case 4: return dense_mfma_ks<4, MODE>(L, xh, xl, xs, B, sg, total, resid);
-        case 8: return dense_mfma_ks<8, MODE>(L, xh, xl, xs, B, sg, total, resid);
-        case 16: return dense_mfma_ks<16, MODE>(L, xh, xl, xs, B, sg, total, resid);
+        case 1: return dense_mfma_ks<1, MODE>(L, xh, xl, B, sg, total, resid);
+        case 2: return dense_mfma_ks<2, MODE>(L, xh, xl, B, sg, total, resid);
+        case 4: return dense_mfma_ks<4, MODE>(L, xh, xl, B, sg, total, resid);
+        case 8: return dense_mfma_ks<8, MODE>(L, xh, xl, B, sg, total, resid);
+        case 16: return dense_mfma_ks<16, MODE>(L, xh, xl, B, sg, total, resid);
         default: return hipErrorNotSupported;
     }
 }
 }  // namespace
 
-hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16_t *x_lo, int x_stride, int B,
-                             int K, const void *const W[3], float *const out[3], const int rows[3], float *resid) {
+hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16_t *x_lo, int B, int K,
+                             const void *const W[3], float *const out[3], const int rows[3], float *resid) {
     Segs sg;
     int total = 0;
     for (int i = 0; i < 3; ++i) {
@@ -1157,9 +1157,8 @@ hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16
     if (total == 0 || B == 0) return hipSuccess;
     if (!dense_mfma_supported(RBT_DT_BF16, B, K, W, rows) || (resid && rows[1] + rows[2] != 0))
         return hipErrorNotSupported;
-    if (x_stride < K || x_stride % 8 != 0) return hipErrorInvalidValue;
-    return resid ? dense_mfma_mode<1>(L, x_hi, x_lo, x_stride, B, K, sg, total, resid)
-                 : dense_mfma_mode<0>(L, x_hi, x_lo, x_stride, B, K, sg, total, nullptr);
+    return resid ? dense_mfma_mode<1>(L, x_hi, x_lo, B, K, sg, total, resid)
+                 : dense_mfma_mode<0>(L, x_hi, x_lo, B, K, sg, total, nullptr);
 }
 
 hipError_t launch_dense_batch(const Launch &L, int dtype, const float *xin, int B, int D, const void *const W[3],
@@ -1265,10 +1264,11 @@ hipError_t launch_attention(const Launch &L, const float *q, const float *k, con
 }
 
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,
-                             uint16_t *ao_hi, uint16_t *ao_lo, int plane_stride) {
-    if ((ao_hi == nullptr) != (ao_lo == nullptr) || (ao_hi && plane_stride < n_heads * hd)) return hipErrorInvalidValue;
+                             uint16_t *ao_hi, uint16_t *ao_lo) {
+    if ((ao_hi == nullptr) != (ao_lo == nullptr) || (ao_hi && (B > 64 || (n_heads * hd) % 32 != 0)))
+        return hipErrorInvalidValue;
     return launch(L, attn_merge_kernel, dim3((unsigned)n_heads, (unsigned)B), dim3(256), 0, part, hd, S, ao, ao_hi,
-                  ao_lo, plane_stride);
+                  ao_lo);
 }
 
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x) {
@@ -1284,10 +1284,9 @@ hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, con
 }
 
 hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B,
-                          uint16_t *out_hi, uint16_t *out_lo, int plane_stride) {
-    if ((out_hi == nullptr) != (out_lo == nullptr) || (out_hi && plane_stride < n)) return hipErrorInvalidValue;
-    return launch(L, rmsnorm_kernel, dim3((unsigned)B), dim3(1024), 0, x, w, n, eps, out, out_hi, out_lo,
-                  plane_stride);
+                          uint16_t *out_hi, uint16_t *out_lo) {
+    if ((out_hi == nullptr) != (out_lo == nullptr) || (out_hi && (B > 64 || n % 32 != 0))) return hipErrorInvalidValue;
+    return launch(L, rmsnorm_kernel, dim3((unsigned)B), dim3(1024), 0, x, w, n, eps, out, out_hi, out_lo);
 }
 
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B) {

@@ -209,26 +209,32 @@ hipError_t launch_attention(const Launch &L, const float *q, const float *k, con
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
                             float *part, int B);
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,
-                             uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr, int plane_stride = 0);
+                             uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr);
 // Dense rows over B token vectors xin [B][D] (batched decode): out_s [B][rows_s], or with resid != NULL
 // resid [B][rows] += (one segment). Same row shapes as dense_supported.
 hipError_t launch_dense_batch(const Launch &L, int dtype, const float *xin, int B, int D, const void *const W[3],
                               float *const out[3], const int rows[3], float *resid);
 hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, const void *Wo, int D, float *x);
-// out_hi / out_lo (may be null): the rows' bf16 hi and lo parts as well (launch_dense_mfma's input), rows
-// plane_stride elements apart.
+// out_hi / out_lo (may be null): the rows' bf16 hi and lo parts as well, as matrix-core planes
+// (mfma_plane_index; n a multiple of 32).
 hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B,
-                          uint16_t *out_hi = nullptr, uint16_t *out_lo = nullptr, int plane_stride = 0);
-// launch_dense_batch on the matrix cores: B <= 64 token rows given as bf16 hi/lo planes [B][K]; bf16
+                          uint16_t *out_hi = nullptr, uint16_t *out_lo = nullptr);
+// launch_dense_batch on the matrix cores: B <= 64 token rows given as bf16 hi/lo planes (mfma_plane_index); bf16
 // weights only, K = 128 * {1, 2, 4, 8, 16}, every segment a multiple of 16 rows
 // (dense_mfma_supported). The products are exact; the sums run in the MFMA order, then the slices of
 // K in a fixed order.
 bool dense_mfma_supported(int dtype, int B, int K, const void *const W[3], const int rows[3]);
-hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16_t *x_lo, int x_stride, int B,
-                             int K, const void *const W[3], float *const out[3], const int rows[3], float *resid);
-// Row stride of the hi/lo planes for rows of n elements: 128 bytes more than a multiple of 4 KiB, so the
-// rows that one load instruction touches fall on different L2 channels.
-inline int mfma_plane_stride(int n) { return (n + 2047) / 2048 * 2048 + 64; }
+hipError_t launch_dense_mfma(const Launch &L, const uint16_t *x_hi, const uint16_t *x_lo, int B, int K,
+                             const void *const W[3], float *const out[3], const int rows[3], float *resid);
+// The bf16 hi/lo planes of B <= 64 token rows of K elements (K a multiple of 32) in the order the matrix
+// cores take their B operand: one 1 KiB tile per (k-step of 32, block of 16 tokens), k-step-major;
+// inside a tile, lane (t % 16) + 16 * ((k % 32) / 8) holds token t's 8 elements from k - k % 8 on.
+// A wave's load of one operand tile is then one contiguous 1 KiB. Tiles of a partial token block are
+// whole (their unused lanes are never written and only feed outputs that are dropped).
+inline size_t mfma_plane_elems(int B, int K) { return (size_t)K * (size_t)((B + 15) / 16) * 16; }
+__device__ __forceinline__ size_t mfma_plane_index(int t, int k, int TB) {
+    return ((size_t)(k >> 5) * (size_t)TB + (size_t)(t >> 4)) * 512 + (size_t)(((t & 15) + 16 * ((k >> 3) & 3)) * 8 + (k & 7));
+}
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B);
 hipError_t launch_advance(const Launch &L, StepState *st, int B);
 
