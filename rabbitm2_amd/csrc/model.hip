@@ -507,6 +507,31 @@ __device__ __forceinline__ void attn_load_round(float (&kr)[kAttnKG][AE], float 
     }
 }
 
+// hd = 128 (AE = 0): a wave takes 8 positions per round, 8 lanes per position. Lane (g, j) = (l / 8,
+// l % 8) holds the 16 elements 32 i + 4 j + c (i, c < 4) of row g, so each of a row's four 16-byte
+// loads covers whole 128-byte lines, a score is 16 products and a 3-step sum over the lane's group, and
+// each group runs its own online softmax over the positions tb + g of the wave's rounds: two exps per
+// round instead of nine (the layout with a row spread over the wave spent ~590 VALU instructions per
+// 8-position round and stalled at 5.5 TB/s on its arithmetic). The 32 (wave, group) partials of a
+// block merge at its end through LDS.
+constexpr int kAttnG8Hd = 128;
+constexpr int kAttnG8Pos = 8;  // positions per wave-round
+static_assert(kAttnG8Pos == kAttnKG, "the first round's prefetch is shared by both layouts");
+__device__ __forceinline__ float group8_sum(float v) {  // sum over the lane's aligned group of 8
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    return v + dpp_f<kDppHalfMirror>(v);
+}
+__device__ __forceinline__ void attn_g8_load(f32x4 (&kr)[4], f32x4 (&vr)[4], const float *kc, const float *vc, int t,
+                                             int kv_dim, int kvh, int j) {
+    const size_t o = (size_t)t * kv_dim + (size_t)kvh * kAttnG8Hd + 4 * j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        kr[i] = *reinterpret_cast<const f32x4 *>(kc + o + 32 * i);
+        vr[i] = *reinterpret_cast<const f32x4 *>(vc + o + 32 * i);
+    }
+}
+
 template <int AE>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_raw, const float *__restrict__ k_raw,
                                                    const float *__restrict__ v_raw, const float *__restrict__ qw,
@@ -553,9 +578,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
     const int n = pos + 1;
     const int chunk = (n + S - 1) / S;
     const int t0 = min(n, s * chunk), t1 = min(n, t0 + chunk);
-    float kr[kAttnKG][AE], vr[kAttnKG][AE];
-    const int tb0 = t0 + wv * kAttnKG;
-    if (tb0 < t1) attn_load_round(kr, vr, kc, vc, tb0, t1, kv_dim, kvh, hd, lane);
+    constexpr int AEr = AE > 0 ? AE : 1;
+    float kr[kAttnKG][AEr], vr[kAttnKG][AEr];
+    f32x4 kg[4], vg[4];  // AE = 0: the first round's rows
+    const int tb0 = t0 + wv * kAttnKG;  // kAttnKG == kAttnG8Pos
+    if constexpr (AE == 0) {
+        if (tb0 < t1) attn_g8_load(kg, vg, kc, vc, min(tb0 + (lane >> 3), t1 - 1), kv_dim, kvh, lane & 7);
+    } else {
+        if (tb0 < t1) attn_load_round(kr, vr, kc, vc, tb0, t1, kv_dim, kvh, hd, lane);
+    }
 
     // ---- QK-norm: both sums of squares in one reduction (per thread in i = tid, tid + 256, ... order)
     float inv_q = 1.0f, inv_k = 1.0f;
@@ -605,7 +636,83 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
         }
     }
     const float scale = 1.0f / sqrtf((float)hd);
-    float q[AE], o[AE];
+    if constexpr (AE == 0) {
+        const int g = lane >> 3, j = lane & 7;
+        f32x4 q4[4], o4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q4[i] = *reinterpret_cast<const f32x4 *>(qh + 32 * i + 4 * j);
+            o4[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        float m = -INFINITY, l = 0.0f;
+        auto step = [&](f32x4 (&kr4)[4], f32x4 (&vr4)[4], int tb) {
+            const int t = tb + g;
+            if (min(t, t1 - 1) == pos) {  // the current position: from LDS, not the cache
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    kr4[i] = *reinterpret_cast<const f32x4 *>(kh + 32 * i + 4 * j);
+                    vr4[i] = *reinterpret_cast<const f32x4 *>(vh + 32 * i + 4 * j);
+                }
+            }
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                d += (q4[i].x * kr4[i].x + q4[i].y * kr4[i].y) + (q4[i].z * kr4[i].z + q4[i].w * kr4[i].w);
+            d = group8_sum(d);
+            const float sc = t < t1 ? d * scale : -INFINITY;  // rows past the share: a repeat, weight 0
+            const float mn = fmaxf(m, sc);
+            const float mref = mn == -INFINITY ? 0.0f : mn;  // no position yet: alpha = p = 0
+            const float alpha = expf(m - mref), p = expf(sc - mref);
+            l = l * alpha + p;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o4[i] = o4[i] * alpha + p * vr4[i];
+            m = mn;
+        };
+        // wave-uniform rounds 4 * kAttnG8Pos positions apart, two per iteration (ping-pong buffers), the
+        // next round's rows in flight during each round's arithmetic
+        f32x4 kb[4], vb[4];
+        for (int tb = tb0; tb < t1; tb += 8 * kAttnG8Pos) {
+            const int tn = tb + 4 * kAttnG8Pos;
+            if (tn < t1) attn_g8_load(kb, vb, kc, vc, min(tn + g, t1 - 1), kv_dim, kvh, j);
+            step(kg, vg, tb);
+            if (tn >= t1) break;
+            const int tn2 = tn + 4 * kAttnG8Pos;
+            if (tn2 < t1) attn_g8_load(kg, vg, kc, vc, min(tn2 + g, t1 - 1), kv_dim, kvh, j);
+            step(kb, vb, tn);
+        }
+        // merge the 32 (wave, group) partials: scales by wave 0, then one element per thread
+        __shared__ float g_m[32], g_l[32], g_a[32];
+        __shared__ __align__(16) float g_o[32][kAttnG8Hd];
+        const int src = wv * 8 + g;
+        if (j == 0) {
+            g_m[src] = m;
+            g_l[src] = l;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4 *>(&g_o[src][32 * i + 4 * j]) = o4[i];
+        __syncthreads();
+        float *po = part + ((size_t)h * S + s) * (hd + 2);
+        if (wv == 0) {
+            const float ms = lane < 32 ? g_m[lane] : -INFINITY, ls = lane < 32 ? g_l[lane] : 0.0f;
+            const float M = wave_max(ms);
+            const float a = ls > 0.0f ? expf(ms - M) : 0.0f;
+            if (lane < 32) g_a[lane] = a;
+            const float L = wave_sum(a * ls);
+            if (lane == 0) {
+                po[0] = M;
+                po[1] = L;
+            }
+        }
+        __syncthreads();
+        if (tid < kAttnG8Hd) {
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int q2 = 0; q2 < 32; ++q2) acc += g_a[q2] * g_o[q2][tid];
+            po[2 + tid] = acc;
+        }
+        return;
+    }
+    float q[AEr], o[AEr];
 #pragma unroll
     for (int e = 0; e < AE; ++e) {
         const int i = lane + kWave * e;
@@ -625,7 +732,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
                 }
             }
         }
-        float kn[kAttnKG][AE], vn[kAttnKG][AE];
+        float kn[kAttnKG][AEr], vn[kAttnKG][AEr];
         const int tn = tb + 4 * kAttnKG;
         if (tn < t1) attn_load_round(kn, vn, kc, vc, tn, t1, kv_dim, kvh, hd, lane);  // the next round, in flight
         float sc[kAttnKG];
@@ -1253,6 +1360,10 @@ hipError_t launch_attention(const Launch &L, const float *q, const float *k, con
                             float *part, int B) {
     if (hd > kWave * kAttnMaxE || S > 64) return hipErrorInvalidValue;
     const dim3 g((unsigned)n_heads, (unsigned)S, (unsigned)B), b(256);
+    const int kvd = n_kv * hd;
+    if (hd == kAttnG8Hd && kvd % 4 == 0 && seq_stride % 4 == 0 && al16(kc) && al16(vc))
+        return launch(L, attn_kernel<0>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
+                      seq_stride, rope_cs, part);
     if (hd <= kWave)
         return launch(L, attn_kernel<1>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
                       seq_stride, rope_cs, part);

@@ -42,6 +42,33 @@ CASES = [("tiny_olmoe_f32", 3, 6), ("ref_odd_shape", 4, 5), ("ref_qknorm_norenor
          ("olmoe_layer_bf16", 16, 3)]
 
 
+def test_forward_batch_long_context_olmoe_heads(dev):
+    """The OLMoE-shaped layer (16 heads x 128, QK-norm) over 1100 positions of two sequences: 16
+    position splits of up to 69 positions, so every wave of the attention blocks takes several rounds
+    of 8 positions and the splits merge; each sequence against the oracle run on it alone at every
+    position (routing identical, logits normwise within 1e-3)."""
+    spec = MANIFEST["cases"]["olmoe_layer_bf16"]
+    conf = dict(spec["config"], max_seq=2048)
+    cfg = po.Config(**conf)
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    B, n = 2, 1100
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, n, seed=11)
+    want = [po.run(model, prompts[b], order=po.ORDER_AVX2, ctx=n) for b in range(B)]
+    dev.batch_init(B, n)
+    for p in range(n):
+        logits, routing = dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
+                                            cfg.top_k)
+        for b in range(B):
+            wl, wr, _ = want[b]
+            assert np.array_equal(routing[:, b, :], wr[p]), f"seq {b} pos {p}"
+            err = normwise_err(logits[b], wl[p])
+            assert err <= LOGIT_RTOL, f"seq {b} pos {p}: logits error {err:.2e}"
+
+
 @pytest.mark.parametrize("case,B,n", CASES, ids=[c[0] + f"_B{c[1]}" for c in CASES])
 def test_forward_batch_matches_each_sequence_alone(dev, case, B, n):
     spec, cfg, model = build(case)
