@@ -338,6 +338,29 @@ int model_alloc(rbt_hip *h) {
 // final: the final norm, lm_head and argmax (which appends the token past the prompt and advances pos);
 // otherwise only pos advances. Everything is enqueued on the handle stream, nothing waits, so a step
 // can be captured into a graph.
+// The MoE block of the batched forward for 2..kRouterDecodeMaxT tokens on the grouped expert path: the
+// RMSNorm and the router logits in one launch (router_decode_kernel<M, true>, 16 x T blocks: xb and
+// the logits), top-k + the activation split, then dispatch, the grouped GEMMs and the combine into x
+// (rabbit2.c:512-542 for each token).
+int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float eps, int T, float *x, float *xb,
+                     int32_t *routing) {
+    if (!ws_reserve(h, T, L->n_experts, L->top_k, L->expert_hidden)) return 0;
+    if (!pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim))) return 0;
+    Workspace &w = h->ws;
+    uint16_t *x_hi = nullptr, *x_lo = nullptr;
+    prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
+    HIP_OK(h, launch_router_norm(lc(h, kProfRouter), x, nw, eps, L->router, L->router_bias, T, L->n_experts, L->dim,
+                                 w.probs, xb));
+    HIP_OK(h, launch_topk_split(lc(h, kProfTopk), w.probs, T, L->n_experts, L->top_k, L->norm_topk, xb, L->dim, routing,
+                                w.weights, x_hi, x_lo));
+    int32_t *counts = nullptr;
+    HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
+                             L->experts, L->expert_stride, xb, T, L->n_experts, L->top_k, L->dim, L->expert_hidden,
+                             routing, w.weights, w.hbuf, w.pre, x, nullptr, &counts, true));
+    h->expert_counts = counts;
+    return prof_collect(h);
+}
+
 int enqueue_step(rbt_hip *h, bool final) {
     const rbt_config &c = h->cfg;
     DecodeState &ds = h->ds;
@@ -416,6 +439,11 @@ int enqueue_step(rbt_hip *h, bool final) {
                                             ml.expert_stride, routing, w.weights, ds.xb, w.hbuf, 1, c.top_k, D,
                                             c.expert_hidden, ds.x, nullptr, w.probs, c.n_experts, c.norm_topk));
             if (!prof_collect(h)) return 0;
+        } else if (B > 1 && B <= kRouterDecodeMaxT && c.n_experts <= 64 &&
+                   router_norm_supported(h->order, c.dtype, B, D, ml.router, ds.x, ffn_norm) &&
+                   prefill_supported(c.dtype, B, h->prefill_min_tokens, c.n_experts, c.top_k, D, c.expert_hidden,
+                                     ml.experts, ml.expert_stride, ds.xb)) {
+            if (!moe_grouped_norm(h, &ml, ffn_norm, c.rms_eps, B, ds.x, ds.xb, routing)) return 0;
         } else {
             STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, ffn_norm, D, c.rms_eps, ds.xb, B));
             if (!rbt_hip_moe_dev(h, &ml, ds.xb, B, ds.x, nullptr, routing, nullptr)) return 0;

@@ -107,6 +107,13 @@ hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype
                          const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,
                          int32_t *routing, float *weights);
 
+// Tokens up to which the AVX2-order router logits run on the decode kernel (16 x T blocks of 64
+// threads; at 32 tokens 5.0 us against 19.9 us for the batch kernel).
+constexpr int kRouterDecodeMaxT = 64;
+// Softmax + top-k of T tokens' logits [T][E] (E <= 64) and the bf16 hi/lo split of their rows xb [T][D]
+// (D % 8 == 0, 16-byte aligned) into x_hi / x_lo [T][D]: one block per token.
+hipError_t launch_topk_split(const Launch &L, const float *logits, int T, int E, int K, int norm_topk, const float *xb,
+                             int D, int32_t *routing, float *weights, uint16_t *x_hi, uint16_t *x_lo);
 // Router logits (AVX2 order, few tokens, bf16) with the RMSNorm in front folded in: x [T][D] is the
 // residual stream and nw the norm weights; token t's xb = x * inv * nw also goes to xb_out [T][D].
 bool router_norm_supported(int order, int dtype, int T, int D, const void *W, const float *x, const float *nw);

@@ -415,6 +415,37 @@ __device__ __forceinline__ void wave_softmax_topk(float v, int E, int K, int nor
     if (lane < K) weights_t[lane] = norm_topk ? s_p[lane] / wsum : s_p[lane];
 }
 
+// Softmax + top-k of token t's E <= 64 logits (wave 0 of block t, the engine's arithmetic as above) and
+// the bf16 hi/lo split of its activation row (every thread, 8 elements per 16-byte pair): the grouped
+// expert path's front end for a few tokens whose logits and normalised rows router_decode_kernel<M,
+// true> has just written (16 x T blocks for the chains instead of the fused prefill kernel's one
+// block per two tokens).
+__global__ __launch_bounds__(256) void topk_split_kernel(const float *__restrict__ logits, int E, int K, int norm_topk,
+                                                         const float *__restrict__ xb, int D,
+                                                         int32_t *__restrict__ routing, float *__restrict__ weights,
+                                                         uint16_t *__restrict__ x_hi, uint16_t *__restrict__ x_lo) {
+    __shared__ __align__(16) float s_v[64];
+    __shared__ float s_p[64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float v = tid < E ? logits[(size_t)t * E + tid] : 0.0f;
+    const size_t row = (size_t)t * D;
+    for (int u = tid; u < D / 8; u += blockDim.x) {
+        const f32x4 a = ld_f4(xb + row + 8 * u), b = ld_f4(xb + row + 8 * u + 4);
+        const float x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t hb[8], lb[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            hb[k] = f32_to_bf16_rne(x8[k]);
+            lb[k] = f32_to_bf16_rne(x8[k] - __uint_as_float(hb[k] << 16));
+        }
+        *reinterpret_cast<u32x4 *>(x_hi + row + 8 * u) =
+            u32x4{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16)};
+        *reinterpret_cast<u32x4 *>(x_lo + row + 8 * u) =
+            u32x4{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16), lb[4] | (lb[5] << 16), lb[6] | (lb[7] << 16)};
+    }
+    if (tid < kWave) wave_softmax_topk(v, E, K, norm_topk, s_v, s_p, routing + (size_t)t * K, weights + (size_t)t * K);
+}
+
 // Prefill front end in one launch (AVX2 order, E <= 64, bf16): router logits, softmax + top-k, and the
 // bf16 hi/lo split of x for the grouped GEMMs. One block per kPTok tokens covers all router rows, so the
 // top-k runs in the block. Wave (token tl, half h) holds the 64 router rows in its lanes and runs
@@ -784,7 +815,7 @@ inline bool decode_ok(int T, int D, int dtype, const void *W, const float *xb) {
     const int m = D / 16;
     const bool m_ok = D % 16 == 0 && (m == 8 || m == 16 || m == 32 || m == 48 || m == 64 || m == 96 || m == 128 ||
                                       m == 192 || m == 256);
-    return T < 16 && dtype == RBT_DT_BF16 && m_ok && (reinterpret_cast<uintptr_t>(W) % 16 == 0) &&
+    return T <= kRouterDecodeMaxT && dtype == RBT_DT_BF16 && m_ok && (reinterpret_cast<uintptr_t>(W) % 16 == 0) &&
            (reinterpret_cast<uintptr_t>(xb) % 16 == 0);
 }
 
@@ -882,6 +913,16 @@ bool router_norm_supported(int order, int dtype, int T, int D, const void *W, co
 hipError_t launch_router_norm(const Launch &L, const float *x, const float *nw, float eps, const void *W,
                               const float *bias, int T, int E, int D, float *logits, float *xb_out) {
     return launch_router_decode_t<true>(L, x, W, bias, T, E, D, logits, nw, eps, xb_out);
+}
+
+hipError_t launch_topk_split(const Launch &L, const float *logits, int T, int E, int K, int norm_topk, const float *xb,
+                             int D, int32_t *routing, float *weights, uint16_t *x_hi, uint16_t *x_lo) {
+    if (T <= 0) return hipSuccess;
+    if (T > 65535 || E < 1 || E > 64 || K < 1 || K > E || D % 8 != 0 ||
+        ((reinterpret_cast<uintptr_t>(xb) | reinterpret_cast<uintptr_t>(x_hi) | reinterpret_cast<uintptr_t>(x_lo)) & 15u))
+        return hipErrorInvalidValue;
+    return launch(L, topk_split_kernel, dim3((unsigned)T), dim3(256), 0, logits, E, K, norm_topk, xb, D, routing,
+                  weights, x_hi, x_lo);
 }
 
 bool router_prefill_supported(int order, int dtype, int T, int E, int D, int K, const void *W, const float *xb) {
