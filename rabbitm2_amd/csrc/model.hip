@@ -340,21 +340,26 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // blocks, all of their activation loads before the first MFMA, so a block costs about one memory round
 // trip. v_mfma_f32_16x16x32_bf16 per (k-step, 16 tokens, part); the NW slices are added in order
 // through LDS. Lane l of a 16 x 16 result holds rows 4 (l / 16) + v, token l % 16.
-// MODE 0: segment outputs; 1: resid[b][r] += (one segment).
+// MODE 0: segment outputs; 1: resid[b][r] += (one segment). SPLIT: the block takes the one token block
+// blockIdx.y (TB = 1) -- for products with few row tiles, so that twice the blocks share the chip and
+// each reads half the planes.
 template <int KS>
 struct MfmaShape {
     static constexpr int NW = KS >= 4 ? 16 : 4 * KS;  // waves per block
     static constexpr int WS = 4 * KS / NW;             // k-steps per wave (1..4)
 };
-template <int KS, int TB, int MODE>
+template <int KS, int TB, int MODE, bool SPLIT = false>
 __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__restrict__ x_hi,
                                                           const uint16_t *__restrict__ x_lo, int B, Segs sg,
                                                           int total_rows, float *__restrict__ resid) {
     constexpr int K = 128 * KS, NW = MfmaShape<KS>::NW, WS = MfmaShape<KS>::WS;
     static_assert(WS >= 1 && WS <= 4 && NW * WS * 32 == K, "k split");
+    static_assert(!SPLIT || TB == 1, "one token block per block");
     __shared__ f32x4 part[NW][TB][kWave];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int row0 = blockIdx.x * 16;
+    const int tbase = SPLIT ? (int)blockIdx.y : 0;  // this block's first token block
+    const int tbt = (B + 15) / 16;                   // token blocks of the planes
     int s = 0, r = row0;  // the tile's segment and first row in it (segments are whole tiles)
     while (s < 2 && r >= sg.rows[s]) {
         r -= sg.rows[s];
@@ -377,7 +382,7 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
             if (tb0 + j < TB) {
 #pragma unroll
                 for (int i = 0; i < WS; ++i) {
-                    const size_t o = (((size_t)(w * WS + i) * TB + (tb0 + j)) * kWave + lane) * 8;
+                    const size_t o = (((size_t)(w * WS + i) * tbt + (tbase + tb0 + j)) * kWave + lane) * 8;
                     bh[i][j] = *reinterpret_cast<const u32x4 *>(x_hi + o);
                     bl[i][j] = *reinterpret_cast<const u32x4 *>(x_lo + o);
                 }
@@ -413,7 +418,7 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
 #pragma unroll
         for (int ww = 1; ww < NW; ++ww) sum = sum + v[ww];
         const int tb = e / (kWave * 4), l = (e / 4) % kWave, j = e % 4;
-        const int t = 16 * tb + (l & 15), rr = 4 * (l >> 4) + j;
+        const int t = 16 * (tbase + tb) + (l & 15), rr = 4 * (l >> 4) + j;
         if (t >= B) continue;
         if constexpr (MODE == 1) {
             float *dst = resid + (size_t)t * total_rows + row0 + rr;
@@ -1225,11 +1230,19 @@ bool dense_mfma_supported(int dtype, int B, int K, const void *const W[3], const
 }
 
 namespace {
+// Row tiles below which a product over two or more token blocks is split by token block: fewer tiles
+// than CUs leave CUs idle (wo at 2048 rows, 128 tiles: 7.7 -> 6.6 us at 32 tokens), while more have
+// each weight row read twice (q/k/v at 6144 rows, 384 tiles: 14.2 -> 16.6 us when split).
+constexpr int kMfmaSplitTiles = 256;
 template <int KS, int MODE>
 hipError_t dense_mfma_ks(const Launch &L, const uint16_t *xh, const uint16_t *xl, int B, const Segs &sg,
                          int total, float *resid) {
     const dim3 g((unsigned)(total / 16)), b(64 * MfmaShape<KS>::NW);
-    switch ((B + 15) / 16) {
+    const int tbt = (B + 15) / 16;
+    if (tbt >= 2 && total / 16 < kMfmaSplitTiles)  // few row tiles: a block per (row tile, token block)
+        return launch(L, dense_mfma_kernel<KS, 1, MODE, true>, dim3((unsigned)(total / 16), (unsigned)tbt), b, 0, xh, xl,
+                      B, sg, total, resid);
+    switch (tbt) {
         case 1: return launch(L, dense_mfma_kernel<KS, 1, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
         case 2: return launch(L, dense_mfma_kernel<KS, 2, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
         case 3: return launch(L, dense_mfma_kernel<KS, 3, MODE>, g, b, 0, xh, xl, B, sg, total, resid);

@@ -36,10 +36,11 @@ def prompts_for(cfg, B, n, seed):
     return rng.integers(0, cfg.vocab, (B, n)).astype(np.int32)
 
 
-# (case, B, positions): tiny models with the per-token fallbacks and the dense batch kernels, and the
-# OLMoE-shaped layer at 16 sequences (grouped MoE path, batched dense matvecs, 16 heads x 128)
+# (case, B, positions): tiny models with the per-token fallbacks and the dense batch kernels, a tiny bf16
+# model (8 experts, top-2) and the OLMoE-shaped layer at 16 sequences (grouped MoE path behind the
+# decode router kernel and the top-k + split launch, batched dense matvecs, 16 heads x 128)
 CASES = [("tiny_olmoe_f32", 3, 6), ("ref_odd_shape", 4, 5), ("ref_qknorm_norenorm", 5, 5),
-         ("olmoe_layer_bf16", 16, 3)]
+         ("tiny_olmoe_bf16", 16, 4), ("olmoe_layer_bf16", 16, 3)]
 
 
 def test_forward_batch_long_context_olmoe_heads(dev):
@@ -87,12 +88,21 @@ def test_forward_batch_matches_each_sequence_alone(dev, case, B, n):
             assert err <= LOGIT_RTOL, f"{case} seq {b} pos {p}: logits error {err:.2e}"
 
 
-@pytest.mark.parametrize("B", [33, 64])
-def test_batch_matrix_core_matvecs_agree_with_vector_ones(dev, B):
+@pytest.mark.parametrize("B,vocab", [(33, 256), (64, 256), (33, 8192)])
+def test_batch_matrix_core_matvecs_agree_with_vector_ones(dev, B, vocab):
     """The batched q/k/v, wo and lm_head on the matrix cores (option batch_mfma, the default; B = 33 fills
     a last block of 16 tokens with one sequence) against the VALU dot products: routing identical,
-    logits within rounding of each other, and the first and last sequences against the oracle."""
-    spec, cfg, model = build("olmoe_layer_bf16")
+    logits within rounding of each other, and the first and last sequences against the oracle. Below 256
+    row tiles of 16 (wo, and lm_head at vocab 256) a block takes one 16-token block, from 256 on (q/k/v,
+    lm_head at vocab 8192) every token block."""
+    if vocab == 256:
+        spec, cfg, model = build("olmoe_layer_bf16")
+    else:
+        spec = MANIFEST["cases"]["olmoe_layer_bf16"]
+        cfg = po.Config(**dict(spec["config"], vocab=vocab))
+        g = spec["gen_params"]
+        model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                                 emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
     dev.upload(model)
     dev.set_router_order(po.ORDER_AVX2)
     prompts = prompts_for(cfg, B, 2, seed=B + 100)
@@ -115,6 +125,30 @@ def test_batch_matrix_core_matvecs_agree_with_vector_ones(dev, B):
         for p in range(2):
             assert np.array_equal(runs[1][p][1][:, b, :], wr[p])
             assert normwise_err(runs[1][p][0][b], wl[p]) <= LOGIT_RTOL
+
+
+def test_forward_batch_grouped_front_end_renormalised(dev):
+    """The grouped MoE path of the batched forward with renormalised top-k weights (norm_topk = 1) and
+    20 sequences: the router kernel's logits, the per-token top-k + split launch and the combine
+    against the oracle run on each sequence alone."""
+    spec = MANIFEST["cases"]["tiny_olmoe_bf16"]
+    cfg = po.Config(**dict(spec["config"], norm_topk=1))
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"] + 7, w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    B, n = 20, 3
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, n, seed=21)
+    want = [po.run(model, prompts[b], order=po.ORDER_AVX2) for b in range(B)]
+    dev.batch_init(B, 0)
+    for p in range(n):
+        logits, routing = dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
+                                            cfg.top_k)
+        for b in range(B):
+            wl, wr, _ = want[b]
+            assert np.array_equal(routing[:, b, :], wr[p]), f"seq {b} pos {p}"
+            assert normwise_err(logits[b], wl[p]) <= LOGIT_RTOL, f"seq {b} pos {p}"
 
 
 def test_forward_batch_sequences_restart_independently(dev):
