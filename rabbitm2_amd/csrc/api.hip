@@ -756,7 +756,14 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
         // kernels (the grouped path then splits the activations itself)
         const bool fused = router_prefill_supported(h->order, L->dtype, T, L->n_experts, L->dim, L->top_k,
                                                     L->router, xb_dev);
-        if (fused) {
+        if (fused && T <= kRouterDecodeMaxT) {  // few tokens: decode router kernel, then top-k + split
+            uint16_t *x_hi = nullptr, *x_lo = nullptr;
+            prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
+            HIP_OK(h, launch_router_logits(lc(h, kProfRouter), h->order, L->dtype, xb_dev, L->router, L->router_bias, T,
+                                           L->n_experts, L->dim, w.probs));
+            HIP_OK(h, launch_topk_split(lc(h, kProfTopk), w.probs, T, L->n_experts, L->top_k, L->norm_topk, xb_dev, L->dim,
+                                        routing, weights, x_hi, x_lo));
+        } else if (fused) {
             uint16_t *x_hi = nullptr, *x_lo = nullptr;
             prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
             HIP_OK(h, launch_router_prefill(lc(h, kProfRouter), L->dtype, xb_dev, L->router, L->router_bias, T,
