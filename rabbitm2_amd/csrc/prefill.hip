@@ -32,14 +32,13 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kMT = 64;  // rows (pairs) per tile
 constexpr int kDispatchMaxE = 256;
 
 
 // ---------------------------------------------------------------- dispatch (one block, 1024 threads)
 // routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);
 // perm[P]: pair ids grouped by expert, increasing within an expert; pos_of[P]: inverse of perm;
-// m_off[E+1]: exclusive prefix of ceil(counts / kMT).
+// m_off[E+1]: exclusive prefix of ceil(counts / mt_rows) (the grouped GEMMs' row tiles per expert).
 // Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
 // equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
 // row; a pair's rank inside its wave's slice goes to pos_of as a temporary. B: wave 0 (4 experts per
@@ -48,7 +47,7 @@ constexpr int kDispatchMaxE = 256;
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ routing, int P, int E,
                                                         int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ perm, int32_t *__restrict__ pos_of,
-                                                        int32_t *__restrict__ m_off) {
+                                                        int32_t *__restrict__ m_off, int mt_rows) {
     constexpr int NW = 16;
     __shared__ int s_w[NW][kDispatchMaxE];  // A: running counts per wave; B: each wave's base positions
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -83,7 +82,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
             if (e < E)
                 for (int w = 0; w < NW; ++w) tot += s_w[w][e];
             c[i] = tot;
-            mt[i] = (tot + kMT - 1) / kMT;
+            mt[i] = (tot + mt_rows - 1) / mt_rows;
         }
         // exclusive scans across the wave of the lanes' sums (4 experts per lane, ascending)
         int sc = ((c[0] + c[1]) + c[2]) + c[3], sm = ((mt[0] + mt[1]) + mt[2]) + mt[3];
@@ -166,46 +165,61 @@ __device__ __forceinline__ void wait_dma() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Tile: 64 list rows x 256 weight rows (gate/up: 128 of W1 and the same 128 of W3; down: 256 of W2),
-// reduction in chunks of 64 (128 bytes of each bf16 row). A chunk is one ring stage in LDS:
-//   weights  256 rows x 128 B   (32 KiB)
-//   act hi    64 rows x 128 B   ( 8 KiB)   bf16 hi plane of the 64 activation rows
-//   act lo    64 rows x 128 B   ( 8 KiB)
-// Three stages (144 KiB): while the MFMAs run on stage c, the copies of stages c+1 and c+2 are in flight.
+// Tile: ROWS list rows (64, or 32 for decode-sized batches) x 256 weight rows (gate/up: 128 of W1 and
+// the same 128 of W3; down: 256 of W2), reduction in chunks of 64 (128 bytes of each bf16 row). A chunk
+// is one ring stage in LDS:
+//   weights  256 rows x 128 B     (32 KiB)
+//   act hi   ROWS rows x 128 B    (8 or 4 KiB)   bf16 hi plane of the activation rows
+//   act lo   ROWS rows x 128 B    (8 or 4 KiB)
+// ROWS = 64: three stages (144 KiB), the copies of stages c+1 and c+2 in flight while the MFMAs run on
+// stage c. ROWS = 32: four stages (160 KiB), three in flight. The kernel is bound by its copies (it
+// keeps 90% of its time with the MFMAs and operand reads taken out), but not by how many are in flight:
+// a stage takes ~1.46 us with two or three ahead (32 decode tokens: 96.7 -> 93.3 us for gate/up).
 // Inside a stage, row r's 16-byte granule g sits at slot g ^ ((r >> 1) & 7) of the row: the MFMA
 // operand reads (16 consecutive rows at one granule per 16 lanes) then hit 16 distinct bank groups.
-// Copies: per stage 32 weight + 16 activation instructions of 8 rows x 128 B, 6 per wave.
-constexpr int kGRows = kMT, kGWRows = 256, kGKC = 64, kGStages = 3;
-constexpr int kGWBytes = kGWRows * 128, kGABytes = kGRows * 128;
-constexpr int kGStageBytes = kGWBytes + 2 * kGABytes;  // 48 KiB
-constexpr int kGRG = kGRows / 16;       // row groups of 16 (one per wave)
-constexpr int kGCH = 8 / kGRG;          // weight-row splits (waves per row group)
-constexpr int kGWI = kGWRows / 64;      // weight copies per wave per stage
-constexpr int kGAI = kGRows / 32;       // activation copies per wave per stage
-constexpr int kGDmaPerWave = kGWI + kGAI;
-static_assert(kGStageBytes == 48 * 1024 && kGDmaPerWave == 6 && kGWRows / 16 / kGCH == 8, "tile shape");
+// Copies: per stage 32 weight + ROWS / 4 activation instructions of 8 rows x 128 B, 4 + ROWS / 32 per wave.
+constexpr int kGWRows = 256, kGKC = 64;
+constexpr int kSmallTileRowsPerExpert = 16;  // mean list rows per expert up to which tiles have 32 rows
+constexpr int kGWBytes = kGWRows * 128;
+constexpr int kGWI = kGWRows / 64;  // weight copies per wave per stage
+template <int ROWS>
+struct GTile {
+    static constexpr int kStages = ROWS == 64 ? 3 : 4;
+    static constexpr int kABytes = ROWS * 128;
+    static constexpr int kStageBytes = kGWBytes + 2 * kABytes;
+    static constexpr int kRG = ROWS / 16;             // row groups of 16 (one per wave)
+    static constexpr int kCH = 8 / kRG;               // weight-row splits (waves per row group)
+    static constexpr int kNB = kGWRows / 16 / kCH;    // weight blocks of 16 per wave
+    static constexpr int kAI = ROWS / 32;             // activation copies per wave per stage
+    static constexpr int kDmaPerWave = kGWI + kAI;
+    static_assert((ROWS == 64 || ROWS == 32) && kStages * kStageBytes <= 160 * 1024 && kAI * 8 * 8 == 2 * ROWS,
+                  "tile shape");
+};
 
 __device__ __forceinline__ int swz(int r, int g) { return g ^ ((r >> 1) & 7); }
 
 // MATS = 2: h = silu(W1 a) * (W3 a) for a = xb rows gathered through perm (N = H columns, Kd = D),
 //           written as bf16 hi/lo planes [P][N] (the next GEMM's activation operand).
 // MATS = 1: y = W2 a for a = the h planes in list order (N = D, Kd = H), written as f32 [P][N].
-// Waves: w = 4*ch + rg computes list rows [16 rg, +16) x the ch-th half of the tile's weight rows
-// (8 blocks of 16: gate/up W1 blocks 4ch..4ch+3 and the matching W3 blocks; down W2 blocks 8ch..8ch+7).
+// Waves: w = kRG*ch + rg computes list rows [16 rg, +16) x the ch-th of kCH parts of the tile's weight
+// rows (kNB blocks of 16: gate/up W1 blocks (kNB/2) ch .. and the matching W3 blocks; down W2 blocks
+// kNB ch ..).
 // Requirements (prefill_supported): N % (256 / MATS) == 0, Kd % 64 == 0, 16-byte aligned rows.
-template <int MATS>
+template <int MATS, int ROWS>
 __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
     int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
     uint16_t *__restrict__ out_lo) {
+    using TS = GTile<ROWS>;
     constexpr int NTILE = kGWRows / MATS;  // output columns per tile
-    __shared__ __align__(1024) uint8_t ring[kGStages * kGStageBytes];
+    constexpr int STAGES = TS::kStages, SBYTES = TS::kStageBytes, NB = TS::kNB, AI = TS::kAI;
+    __shared__ __align__(1024) uint8_t ring[STAGES * SBYTES];
 
     // w in a scalar register: the branches on it below are then wave-uniform jumps, not exec masks
-    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), rg = w % kGRG,
-              ch = w / kGRG;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), rg = w % TS::kRG,
+              ch = w / TS::kRG;
     const int ntiles_n = N / NTILE;
     const int total = m_off[E] * ntiles_n;
     const int range = (total + 7) >> 3;
@@ -224,8 +238,8 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     const int me = m_off[e + 1] - m_off[e];
     const int local = tau - m_off[e] * ntiles_n;
     const int jt = local / me, il = local - jt * me;
-    const int row0 = offsets[e] + il * kGRows;
-    const int rows = min(kGRows, counts[e] - il * kGRows);
+    const int row0 = offsets[e] + il * ROWS;
+    const int rows = min(ROWS, counts[e] - il * ROWS);
     const int n0 = jt * NTILE;
     const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
 
@@ -244,11 +258,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
         }
         wsrc[i] = base + (size_t)wr * rowb + 16 * g;
     }
-    const uint8_t *asrc[kGAI];
+    const uint8_t *asrc[AI];
 #pragma unroll
-    for (int i = 0; i < kGAI; ++i) {
-        // copy u: plane u / (kGRows / 8), rows 8 * (u % (kGRows / 8)) ..
-        const int u = kGAI * w + i, plane = u / (kGRows / 8), r = 8 * (u % (kGRows / 8)) + (lane >> 3),
+    for (int i = 0; i < AI; ++i) {
+        // copy u: plane u / (ROWS / 8), rows 8 * (u % (ROWS / 8)) ..
+        const int u = AI * w + i, plane = u / (ROWS / 8), r = 8 * (u % (ROWS / 8)) + (lane >> 3),
                   g = swz(r, lane & 7);
         const int lr = row0 + (r < rows ? r : 0);  // rows past the list re-read its first row
         const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
@@ -263,55 +277,58 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     // second reads hit L2); the per-output summation order is still fixed for a given input.
     const int rot = (e * ntiles_n + jt) % nch;
     auto issue = [&](int c) {
-        const uint32_t sb = ring0 + (uint32_t)((c % kGStages) * kGStageBytes);
+        const uint32_t sb = ring0 + (uint32_t)((c % STAGES) * SBYTES);
         const int cc = c + rot < nch ? c + rot : c + rot - nch;
         const size_t kb = (size_t)cc * 128;
 #pragma unroll
         for (int i = 0; i < kGWI; ++i)
             lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (kGWI * w + i) * 1024));
 #pragma unroll
-        for (int i = 0; i < kGAI; ++i)
-            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + kGWBytes + (kGAI * w + i) * 1024));
+        for (int i = 0; i < AI; ++i)
+            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + kGWBytes + (AI * w + i) * 1024));
     };
 
     // MFMA operand reads: lane -> row (lane % 16) of a 16-row block, logical granule 4*ks + lane / 16
-    int brow[8];
+    int brow[NB];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < NB; ++q) {
         int blk;
         if constexpr (MATS == 2)
-            blk = q < 4 ? 4 * ch + q : kGWRows / 32 + 4 * ch + (q - 4);
+            blk = q < NB / 2 ? (NB / 2) * ch + q : kGWRows / 32 + (NB / 2) * ch + (q - NB / 2);
         else
-            blk = 8 * ch + q;
+            blk = NB * ch + q;
         brow[q] = blk * 16 + (lane & 15);
     }
     const int arw = 16 * rg + (lane & 15);
     const bool active = 16 * rg < rows;  // wave-uniform: this wave's 16 rows hold list entries
 
-    f32x4 acc[8];
+    f32x4 acc[NB];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q = 0; q < NB; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    issue(0);
-    if (nch > 1) issue(1);
+    for (int c = 0; c < STAGES - 1 && c < nch; ++c) issue(c);
     for (int c = 0; c < nch; ++c) {
-        if (c + 1 < nch)
-            wait_dma<kGDmaPerWave>();  // stage c+1 may still be in flight
+        // stages c+1 .. c+STAGES-2 (as far as they exist) may still be in flight, stage c must have landed
+        const int ahead = min(STAGES - 2, nch - 1 - c);
+        if (ahead >= 2)
+            wait_dma<2 * TS::kDmaPerWave>();
+        else if (ahead == 1)
+            wait_dma<TS::kDmaPerWave>();
         else
             wait_dma<0>();
         __syncthreads();  // every wave's copies of stage c have landed
-        if (c + 2 < nch) issue(c + 2);  // into the stage read at c-1: all waves are past it
+        if (c + STAGES - 1 < nch) issue(c + STAGES - 1);  // into the stage read at c-1: all waves are past it
         if (active) {
-            const uint8_t *st = ring + (c % kGStages) * kGStageBytes;
+            const uint8_t *st = ring + (c % STAGES) * SBYTES;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const int g = 4 * ks + (lane >> 4);
                 const bf16x8 ah =
                     __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + arw * 128 + 16 * swz(arw, g)));
                 const bf16x8 al = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + kGABytes + arw * 128 + 16 * swz(arw, g)));
+                    bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + TS::kABytes + arw * 128 + 16 * swz(arw, g)));
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
+                for (int q = 0; q < NB; ++q) {
                     const bf16x8 bv =
                         __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + brow[q] * 128 + 16 * swz(brow[q], g)));
                     acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, acc[q], 0, 0, 0);
@@ -330,18 +347,18 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
         const size_t orow = (size_t)(row0 + r) * N;
         if constexpr (MATS == 2) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float g = acc[q][i], u = acc[q + 4][i];
+            for (int q = 0; q < NB / 2; ++q) {
+                const float g = acc[q][i], u = acc[q + NB / 2][i];
                 const float v = (g / (1.0f + expf(-g))) * u;  // silu(g) * u, rabbit2.c:535-537
                 const uint32_t hb = f32_to_bf16_rne(v);
                 const uint32_t lb = f32_to_bf16_rne(v - __uint_as_float(hb << 16));
-                const size_t o = orow + n0 + (4 * ch + q) * 16 + (lane & 15);
+                const size_t o = orow + n0 + ((NB / 2) * ch + q) * 16 + (lane & 15);
                 out_hi[o] = (uint16_t)hb;
                 out_lo[o] = (uint16_t)lb;
             }
         } else {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) out_f32[orow + n0 + (8 * ch + q) * 16 + (lane & 15)] = acc[q][i];
+            for (int q = 0; q < NB; ++q) out_f32[orow + n0 + (NB * ch + q) * 16 + (lane & 15)] = acc[q][i];
         }
     }
 }
@@ -385,7 +402,7 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restri
     if (x_inout) x_inout[o] = xo + moe;
 }
 
-template <int MATS>
+template <int MATS, int ROWS>
 hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
                        int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
                        int topk, const int32_t *counts, const int32_t *offsets, const int32_t *m_off, int E,
@@ -393,7 +410,7 @@ hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride,
     const long long tiles = (long long)max_mtiles * (N / (kGWRows / MATS));
     const long long blocks = (tiles + 7) / 8 * 8;
     if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
-    return launch(L, grouped_gemm_kernel<MATS>, dim3((unsigned)blocks), dim3(512), 0, experts, stride, w_off, w3_off,
+    return launch(L, grouped_gemm_kernel<MATS, ROWS>, dim3((unsigned)blocks), dim3(512), 0, experts, stride, w_off, w3_off,
                   N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, out_f32, out_hi, out_lo);
 }
 
@@ -473,17 +490,26 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
         e = launch(Ls, split_hilo_kernel, dim3(sblocks), dim3(256), 0, xb, n8, x_hi, x_lo);
         if (e != hipSuccess) return e;
     }
-    e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off);
+    // row tiles of 32 when experts average at most 16 rows (decode-sized batches: a deeper copy ring),
+    // of 64 otherwise (fewer tiles, each weight tile read once per 64 rows)
+    const bool small = P <= kSmallTileRowsPerExpert * E;
+    const int mt_rows = small ? 32 : 64;
+    e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off,
+               mt_rows);
     if (e != hipSuccess) return e;
     const uint8_t *ex = static_cast<const uint8_t *>(experts);
-    const int max_mtiles = (P + kGRows - 1) / kGRows + E;  // >= sum over experts of ceil(count / kGRows)
+    const int max_mtiles = (P + mt_rows - 1) / mt_rows + E;  // >= sum over experts of ceil(count / mt_rows)
     // gate/up: N = H, Kd = D, activation rows gathered through perm; h written as hi/lo planes
-    e = launch_gemm<2>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, E,
-                       max_mtiles, nullptr, h_hi, h_lo);
+    e = small ? launch_gemm<2, 32>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets,
+                                   m_off, E, max_mtiles, nullptr, h_hi, h_lo)
+              : launch_gemm<2, 64>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets,
+                                   m_off, E, max_mtiles, nullptr, h_hi, h_lo);
     if (e != hipSuccess) return e;
     // down: N = D, Kd = H, activation rows = the h planes in list order
-    e = launch_gemm<1>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets,
-                       m_off, E, max_mtiles, y, nullptr, nullptr);
+    e = small ? launch_gemm<1, 32>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts,
+                                   offsets, m_off, E, max_mtiles, y, nullptr, nullptr)
+              : launch_gemm<1, 64>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts,
+                                   offsets, m_off, E, max_mtiles, y, nullptr, nullptr);
     if (e != hipSuccess) return e;
     return launch(Lc, combine_rows_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)T), dim3(256), 0,
                   (const float *)y, (const int32_t *)pos_of, weights, K, D, x_inout, moe_out);
