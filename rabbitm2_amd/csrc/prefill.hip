@@ -165,38 +165,46 @@ __device__ __forceinline__ void wait_dma() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Tile: ROWS list rows (64, or 32 for decode-sized batches) x 256 weight rows (gate/up: 128 of W1 and
-// the same 128 of W3; down: 256 of W2), reduction in chunks of 64 (128 bytes of each bf16 row). A chunk
-// is one ring stage in LDS:
-//   weights  256 rows x 128 B     (32 KiB)
-//   act hi   ROWS rows x 128 B    (8 or 4 KiB)   bf16 hi plane of the activation rows
-//   act lo   ROWS rows x 128 B    (8 or 4 KiB)
-// ROWS = 64: three stages (144 KiB), the copies of stages c+1 and c+2 in flight while the MFMAs run on
-// stage c. ROWS = 32: four stages (160 KiB), three in flight. The kernel is bound by its copies (it
-// keeps 90% of its time with the MFMAs and operand reads taken out), but not by how many are in flight:
-// a stage takes ~1.46 us with two or three ahead (32 decode tokens: 96.7 -> 93.3 us for gate/up).
-// Inside a stage, row r's 16-byte granule g sits at slot g ^ ((r >> 1) & 7) of the row: the MFMA
-// operand reads (16 consecutive rows at one granule per 16 lanes) then hit 16 distinct bank groups.
-// Copies: per stage 32 weight + ROWS / 4 activation instructions of 8 rows x 128 B, 4 + ROWS / 32 per wave.
-constexpr int kGWRows = 256, kGKC = 64;
+// Tile: ROWS list rows x WROWS weight rows (gate/up: half W1 rows, the same rows of W3; down: W2
+// rows), the reduction in chunks that are one ring stage in LDS each; three stages, the copies of
+// stages c+1 and c+2 in flight while the MFMAs run on stage c:
+//   ROWS = 64: 256 weight rows x 128 B (k-chunks of 64) + 2 x 64 activation rows x 128 B = 48 KiB
+//   ROWS = 32: 128 weight rows x 256 B (k-chunks of 128) + 2 x 32 activation rows x 256 B = 48 KiB
+// (the activation rows: bf16 hi and lo planes). The kernel is bound by its copies: it keeps 90% of
+// its time with the MFMAs and operand reads taken out, and a stage takes ~1.45 us whether two or
+// three stages are in flight and whether a row is read in 128- or 256-byte runs. At 5.8 TB/s of
+// weights it runs at ~94% of what one block per CU streams with plain loads of 32 KiB steps (6.2
+// TB/s, measured for 512 and 1024 threads and runs of 128 B to 1 KiB); the LDS ring leaves no room
+// for a second block. Copies: 1 KiB each (8 rows of 128 B or 4 of 256 B), 4 weight + 2 activation
+// per wave.
+constexpr int kGWRows = 256, kGKC = 64;  // the 64-row tile; prefill_supported's shape rules
 constexpr int kSmallTileRowsPerExpert = 16;  // mean list rows per expert up to which tiles have 32 rows
-constexpr int kGWBytes = kGWRows * 128;
-constexpr int kGWI = kGWRows / 64;  // weight copies per wave per stage
 template <int ROWS>
 struct GTile {
-    static constexpr int kStages = ROWS == 64 ? 3 : 4;
-    static constexpr int kABytes = ROWS * 128;
-    static constexpr int kStageBytes = kGWBytes + 2 * kABytes;
-    static constexpr int kRG = ROWS / 16;             // row groups of 16 (one per wave)
-    static constexpr int kCH = 8 / kRG;               // weight-row splits (waves per row group)
-    static constexpr int kNB = kGWRows / 16 / kCH;    // weight blocks of 16 per wave
-    static constexpr int kAI = ROWS / 32;             // activation copies per wave per stage
-    static constexpr int kDmaPerWave = kGWI + kAI;
-    static_assert((ROWS == 64 || ROWS == 32) && kStages * kStageBytes <= 160 * 1024 && kAI * 8 * 8 == 2 * ROWS,
+    static constexpr int kWRows = ROWS == 64 ? 256 : 128;  // weight rows per tile
+    static constexpr int kKC = ROWS == 64 ? 64 : 128;      // k per stage
+    static constexpr int kRowB = 2 * kKC;                  // bytes of each row per stage
+    static constexpr int kGran = kRowB / 16;               // 16-byte granules per row per stage
+    static constexpr int kRowsPerCopy = 1024 / kRowB;      // rows one 1 KiB copy covers
+    static constexpr int kStages = 3;
+    static constexpr int kWBytes = kWRows * kRowB;         // 32 KiB
+    static constexpr int kABytes = ROWS * kRowB;
+    static constexpr int kStageBytes = kWBytes + 2 * kABytes;
+    static constexpr int kRG = ROWS / 16;                  // row groups of 16 (one per wave)
+    static constexpr int kCH = 8 / kRG;                    // weight-row splits (waves per row group)
+    static constexpr int kNB = kWRows / 16 / kCH;          // weight blocks of 16 per wave
+    static constexpr int kWI = kWBytes / 1024 / 8;         // weight copies per wave per stage
+    static constexpr int kACP = kABytes / 1024;            // copies per activation plane
+    static constexpr int kAI = 2 * kACP / 8;               // activation copies per wave per stage
+    static constexpr int kDmaPerWave = kWI + kAI;
+    static_assert((ROWS == 64 || ROWS == 32) && kStages * kStageBytes <= 160 * 1024 && kAI * 8 == 2 * kACP &&
+                      kWI * 8 * 1024 == kWBytes && kNB >= 2,
                   "tile shape");
+    // Inside a stage, row r's granule g sits at slot swz(r, g): the MFMA operand reads (16 consecutive
+    // rows at one granule per 16 lanes) then hit 16 distinct bank groups (two rows per 256 bytes of
+    // banks for 128-byte rows, one for 256-byte rows).
+    __device__ static int swz(int r, int g) { return kRowB == 128 ? g ^ ((r >> 1) & 7) : g ^ (r & 15); }
 };
-
-__device__ __forceinline__ int swz(int r, int g) { return g ^ ((r >> 1) & 7); }
 
 // MATS = 2: h = silu(W1 a) * (W3 a) for a = xb rows gathered through perm (N = H columns, Kd = D),
 //           written as bf16 hi/lo planes [P][N] (the next GEMM's activation operand).
@@ -213,8 +221,9 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
     uint16_t *__restrict__ out_lo) {
     using TS = GTile<ROWS>;
-    constexpr int NTILE = kGWRows / MATS;  // output columns per tile
-    constexpr int STAGES = TS::kStages, SBYTES = TS::kStageBytes, NB = TS::kNB, AI = TS::kAI;
+    constexpr int WROWS = TS::kWRows, NTILE = WROWS / MATS;  // output columns per tile
+    constexpr int STAGES = TS::kStages, SBYTES = TS::kStageBytes, NB = TS::kNB, AI = TS::kAI, WI = TS::kWI;
+    constexpr int ROWB = TS::kRowB, GRAN = TS::kGran, RPC = TS::kRowsPerCopy, WBYTES = TS::kWBytes;
     __shared__ __align__(1024) uint8_t ring[STAGES * SBYTES];
 
     // w in a scalar register: the branches on it below are then wave-uniform jumps, not exec masks
@@ -244,16 +253,16 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
 
     // copy sources of this lane (one pointer per instruction; each stage adds 128 bytes)
-    const uint8_t *wsrc[kGWI];
+    const uint8_t *wsrc[WI];
 #pragma unroll
-    for (int i = 0; i < kGWI; ++i) {
-        const int t = kGWI * w + i, r = 8 * t + (lane >> 3), g = swz(r, lane & 7);
+    for (int i = 0; i < WI; ++i) {
+        const int t = WI * w + i, r = RPC * t + lane / GRAN, g = TS::swz(r, lane % GRAN);
         const uint8_t *base = experts + (size_t)e * stride + w_off;
         int wr = n0 + r;
         if constexpr (MATS == 2) {
-            if (r >= kGWRows / 2) {
+            if (r >= WROWS / 2) {
                 base = experts + (size_t)e * stride + w3_off;
-                wr = n0 + r - kGWRows / 2;
+                wr = n0 + r - WROWS / 2;
             }
         }
         wsrc[i] = base + (size_t)wr * rowb + 16 * g;
@@ -261,15 +270,15 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     const uint8_t *asrc[AI];
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
-        // copy u: plane u / (ROWS / 8), rows 8 * (u % (ROWS / 8)) ..
-        const int u = AI * w + i, plane = u / (ROWS / 8), r = 8 * (u % (ROWS / 8)) + (lane >> 3),
-                  g = swz(r, lane & 7);
+        // copy u: plane u / kACP, rows RPC * (u % kACP) ..
+        const int u = AI * w + i, plane = u / TS::kACP, r = RPC * (u % TS::kACP) + lane / GRAN,
+                  g = TS::swz(r, lane % GRAN);
         const int lr = row0 + (r < rows ? r : 0);  // rows past the list re-read its first row
         const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
         asrc[i] = reinterpret_cast<const uint8_t *>(plane ? a_lo : a_hi) + arow * rowb + 16 * g;
     }
     const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
-    const int nch = Kd / kGKC;
+    const int nch = Kd / TS::kKC;
     // Stage c reads k-chunk (c + rot) mod nch. Without the rotation every resident block streams the
     // same column window of its rows at the same time, so the whole chip's requests fall on the few
     // DRAM channels that window maps to. The rotation is a function of the weight tile (expert,
@@ -279,13 +288,13 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     auto issue = [&](int c) {
         const uint32_t sb = ring0 + (uint32_t)((c % STAGES) * SBYTES);
         const int cc = c + rot < nch ? c + rot : c + rot - nch;
-        const size_t kb = (size_t)cc * 128;
+        const size_t kb = (size_t)cc * ROWB;
 #pragma unroll
-        for (int i = 0; i < kGWI; ++i)
-            lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (kGWI * w + i) * 1024));
+        for (int i = 0; i < WI; ++i)
+            lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (WI * w + i) * 1024));
 #pragma unroll
         for (int i = 0; i < AI; ++i)
-            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + kGWBytes + (AI * w + i) * 1024));
+            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + WBYTES + (AI * w + i) * 1024));
     };
 
     // MFMA operand reads: lane -> row (lane % 16) of a 16-row block, logical granule 4*ks + lane / 16
@@ -294,7 +303,7 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
     for (int q = 0; q < NB; ++q) {
         int blk;
         if constexpr (MATS == 2)
-            blk = q < NB / 2 ? (NB / 2) * ch + q : kGWRows / 32 + (NB / 2) * ch + (q - NB / 2);
+            blk = q < NB / 2 ? (NB / 2) * ch + q : WROWS / 32 + (NB / 2) * ch + (q - NB / 2);
         else
             blk = NB * ch + q;
         brow[q] = blk * 16 + (lane & 15);
@@ -321,16 +330,16 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
         if (active) {
             const uint8_t *st = ring + (c % STAGES) * SBYTES;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
+            for (int ks = 0; ks < TS::kKC / 32; ++ks) {
                 const int g = 4 * ks + (lane >> 4);
-                const bf16x8 ah =
-                    __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + arw * 128 + 16 * swz(arw, g)));
+                const bf16x8 ah = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(st + WBYTES + arw * ROWB + 16 * TS::swz(arw, g)));
                 const bf16x8 al = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4 *>(st + kGWBytes + TS::kABytes + arw * 128 + 16 * swz(arw, g)));
+                    bf16x8, *reinterpret_cast<const u32x4 *>(st + WBYTES + TS::kABytes + arw * ROWB + 16 * TS::swz(arw, g)));
 #pragma unroll
                 for (int q = 0; q < NB; ++q) {
                     const bf16x8 bv =
-                        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + brow[q] * 128 + 16 * swz(brow[q], g)));
+                        __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + brow[q] * ROWB + 16 * TS::swz(brow[q], g)));
                     acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, acc[q], 0, 0, 0);
                     acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, acc[q], 0, 0, 0);
                 }
@@ -407,7 +416,7 @@ hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride,
                        int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
                        int topk, const int32_t *counts, const int32_t *offsets, const int32_t *m_off, int E,
                        int max_mtiles, float *out_f32, uint16_t *out_hi, uint16_t *out_lo) {
-    const long long tiles = (long long)max_mtiles * (N / (kGWRows / MATS));
+    const long long tiles = (long long)max_mtiles * (N / (GTile<ROWS>::kWRows / MATS));
     const long long blocks = (tiles + 7) / 8 * 8;
     if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
     return launch(L, grouped_gemm_kernel<MATS, ROWS>, dim3((unsigned)blocks), dim3(512), 0, experts, stride, w_off, w3_off,
