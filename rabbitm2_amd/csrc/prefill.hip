@@ -7,7 +7,8 @@
 // (rabbit2.c:173, rabbit2/tools/rbt2.py:152-156), bf16 elements.
 //
 // 1. dispatch_kernel: per-expert lists of the (token, slot) pairs, stable in pair order (counts,
-//    row offsets, perm, inverse perm) and the per-expert count of 64-row tiles.
+//    row offsets, perm, inverse perm) and the per-expert count of row tiles (64 rows, or 32 when the
+//    experts average at most 16 rows).
 // 2. grouped_gemm_kernel<2>: for each expert's rows, h = silu(W1 a) * (W3 a), written as bf16 hi/lo
 //    planes; grouped_gemm_kernel<1>: y = W2 h (f32 rows). Both on v_mfma_f32_16x16x32_bf16.
 //    The f32 activations are split into bf16 hi + lo parts and both parts are multiplied (two MFMAs
@@ -15,8 +16,9 @@
 //    instead of 8. A full 64-row tile then does 64 rows x 2 parts x 2 flop = 256 flop per weight
 //    element, 128 flop per weight byte: below the bf16 MFMA/HBM ridge (2.5 PFLOP/s / 8 TB/s =
 //    312), so the kernels stay bound by HBM.
-//    Tiles: 64 rows x 256 weight rows per block of 8 waves; the reduction runs in chunks of 64
-//    through a three-stage LDS ring filled by direct HBM -> LDS copies (weights and activations).
+//    Tiles: 64 rows x 256 weight rows (or 32 x 128 for decode-sized batches) per block of 8 waves;
+//    the reduction runs in chunks of 64 (128) through a three-stage LDS ring filled by direct
+//    HBM -> LDS copies (weights and activations).
 //    Tile order (expert, column tile, row tile), split into 8 contiguous ranges, one per XCD (the
 //    hardware hands block b to XCD b % 8): the row tiles of a hot expert then share each weight
 //    tile in that XCD's L2, and an expert's activation rows are reused across its column tiles.
