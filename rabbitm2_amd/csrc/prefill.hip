@@ -16,7 +16,8 @@
 //    instead of 8. A full 64-row tile then does 64 rows x 2 parts x 2 flop = 256 flop per weight
 //    element, 128 flop per weight byte: below the bf16 MFMA/HBM ridge (2.5 PFLOP/s / 8 TB/s =
 //    312), so the kernels stay bound by HBM.
-//    Tiles: 64 rows x 256 weight rows (or 32 x 128 for decode-sized batches) per block of 8 waves;
+//    Tiles: 64 rows x 256 weight rows per block of 16 waves (or 32 x 128 per 8 waves for decode-sized
+//    batches);
 //    the reduction runs in chunks of 64 (128) through a three-stage LDS ring filled by direct
 //    HBM -> LDS copies (weights and activations).
 //    Tile order (expert, column tile, row tile), split into 8 contiguous ranges, one per XCD (the
@@ -192,15 +193,16 @@ struct GTile {
     static constexpr int kWBytes = kWRows * kRowB;         // 32 KiB
     static constexpr int kABytes = ROWS * kRowB;
     static constexpr int kStageBytes = kWBytes + 2 * kABytes;
+    static constexpr int kWaves = ROWS == 64 ? 16 : 8;    // waves per block (each needs a W1/W3 pair)
     static constexpr int kRG = ROWS / 16;                  // row groups of 16 (one per wave)
-    static constexpr int kCH = 8 / kRG;                    // weight-row splits (waves per row group)
+    static constexpr int kCH = kWaves / kRG;               // weight-row splits (waves per row group)
     static constexpr int kNB = kWRows / 16 / kCH;          // weight blocks of 16 per wave
-    static constexpr int kWI = kWBytes / 1024 / 8;         // weight copies per wave per stage
+    static constexpr int kWI = kWBytes / 1024 / kWaves;    // weight copies per wave per stage
     static constexpr int kACP = kABytes / 1024;            // copies per activation plane
-    static constexpr int kAI = 2 * kACP / 8;               // activation copies per wave per stage
+    static constexpr int kAI = 2 * kACP / kWaves;          // activation copies per wave per stage
     static constexpr int kDmaPerWave = kWI + kAI;
-    static_assert((ROWS == 64 || ROWS == 32) && kStages * kStageBytes <= 160 * 1024 && kAI * 8 == 2 * kACP &&
-                      kWI * 8 * 1024 == kWBytes && kNB >= 2,
+    static_assert((ROWS == 64 || ROWS == 32) && kStages * kStageBytes <= 160 * 1024 &&
+                      kAI * kWaves == 2 * kACP && kWI * kWaves * 1024 == kWBytes && kNB >= 2 && kNB % 2 == 0,
                   "tile shape");
     // Inside a stage, row r's granule g sits at slot swz(r, g): the MFMA operand reads (16 consecutive
     // rows at one granule per 16 lanes) then hit 16 distinct bank groups (two rows per 256 bytes of
@@ -216,7 +218,7 @@ struct GTile {
 // kNB ch ..).
 // Requirements (prefill_supported): N % (256 / MATS) == 0, Kd % 64 == 0, 16-byte aligned rows.
 template <int MATS, int ROWS>
-__global__ __launch_bounds__(512, 1) void grouped_gemm_kernel(
+__global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kernel(
     const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
     int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
@@ -421,7 +423,8 @@ hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride,
     const long long tiles = (long long)max_mtiles * (N / (GTile<ROWS>::kWRows / MATS));
     const long long blocks = (tiles + 7) / 8 * 8;
     if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
-    return launch(L, grouped_gemm_kernel<MATS, ROWS>, dim3((unsigned)blocks), dim3(512), 0, experts, stride, w_off, w3_off,
+    return launch(L, grouped_gemm_kernel<MATS, ROWS>, dim3((unsigned)blocks), dim3(64 * GTile<ROWS>::kWaves), 0, experts,
+                  stride, w_off, w3_off,
                   N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, out_f32, out_hi, out_lo);
 }
 
