@@ -99,6 +99,9 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode leg")
     ap.add_argument("--profile-forward", type=int, default=0, metavar="N",
                     help="only run N eager forward() steps of the whole model (for kernel traces) and exit")
+    ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
+                    help="only run N eager 512-token calls of layer 0 (uniform, then skewed routing) for kernel "
+                         "traces and exit")
     ap.add_argument("--profile-batch", type=int, default=0, metavar="B",
                     help="with --profile-forward: B sequences per step at the batched leg's context length")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -113,6 +116,9 @@ def main():
 
     if args.profile_forward > 0:
         profile_forward(args.profile_forward, args.profile_batch)
+        return
+    if args.profile_prefill > 0:
+        profile_prefill(args.profile_prefill)
         return
 
     from rabbitm2_amd import hip as rh
@@ -418,6 +424,42 @@ def profile_forward(steps, batch):
             dev.forward_batch(toks, np.full(batch, B_CTX + p, np.int32), cfg.vocab, cfg.n_layers, cfg.top_k)
     dev.synchronize()
     print(f"profile-forward: {steps} eager steps of the 16-layer model (batch {max(batch, 1)}) in "
+          f"{time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
+    dev.close()
+
+
+def profile_prefill(calls):
+    """`calls` eager calls of the prefill leg's workload (512 tokens through layer 0 of the decode
+    stack, same weights and inputs), uniform and then skewed routing, for kernel traces (no HIP
+    graphs, no bench line). Only layer 0's router and experts are filled."""
+    from rabbitm2_amd import hip as rh
+    dev = rh.Device(0)
+    esz = 2
+    stride = (3 * H * D * esz + 4095) // 4096 * 4096
+    routers = dev.malloc(E * D * esz)
+    experts = dev.malloc(E * stride)
+    mat = H * D
+    dev.fill_normal(routers, rh.DT_BF16, E * D, SEED, 16 + 8, scale=W_SCALE)  # layer 0's stream ids
+    for e in range(E):
+        for w in range(3):
+            dev.fill_normal(experts, rh.DT_BF16, mat, SEED, (1 << 32) | (e * 3 + w), scale=W_SCALE,
+                            byte_offset=e * stride + w * mat * esz)
+    T = PREFILL_T
+    xraw = dev.malloc(T * D * 2)
+    dev.fill_normal(xraw, rh.DT_BF16, T * D, SEED, 0x5EED + 1)
+    xs = (dev.d2h(xraw, (T * D,), np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(T, D)
+    xb = dev.upload_array(xs)
+    moe = dev.malloc(T * D * 4)
+    bias_dev = dev.upload_array(np.array([2.0] * 8 + [0.0] * (E - 8), np.float32))
+    dev.set_router_order(rh.ORDER_AVX2)
+    t0 = time.perf_counter()
+    for bias in (None, bias_dev):
+        L = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride, bias)
+        dev.reserve(L, T)
+        for _ in range(calls):
+            dev.moe_dev(L, xb, T, moe=moe)
+        dev.synchronize()
+    print(f"profile-prefill: {calls} eager 512-token calls each with uniform and skewed routing in "
           f"{time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
     dev.close()
 
