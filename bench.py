@@ -99,6 +99,9 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode leg")
     ap.add_argument("--profile-forward", type=int, default=0, metavar="N",
                     help="only run N eager forward() steps of the whole model (for kernel traces) and exit")
+    ap.add_argument("--profile-decode", type=int, default=0, metavar="N",
+                    help="only run N eager decode steps of the 16-layer MoE stack (one weight fill per layer) for "
+                         "kernel traces and exit")
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
                     help="only run N eager 512-token calls of layer 0 (uniform, then skewed routing) for kernel "
                          "traces and exit")
@@ -119,6 +122,9 @@ def main():
         return
     if args.profile_prefill > 0:
         profile_prefill(args.profile_prefill)
+        return
+    if args.profile_decode > 0:
+        profile_decode(args.profile_decode)
         return
 
     from rabbitm2_amd import hip as rh
@@ -425,6 +431,41 @@ def profile_forward(steps, batch):
     dev.synchronize()
     print(f"profile-forward: {steps} eager steps of the 16-layer model (batch {max(batch, 1)}) in "
           f"{time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
+    dev.close()
+
+
+def profile_decode(steps):
+    """`steps` eager decode steps (one token through the 16 MoE layers, the decode leg's kernels and
+    shapes) for kernel traces: no HIP graphs, no bench line. Each layer's router and expert block is
+    filled by one launch (other values than the decode leg's per-expert streams, same sizes)."""
+    from rabbitm2_amd import hip as rh
+    dev = rh.Device(0)
+    esz = 2
+    stride = (3 * H * D * esz + 4095) // 4096 * 4096
+    layer_bytes = E * stride
+    routers = dev.malloc(LAYERS * E * D * esz)
+    experts = dev.malloc(LAYERS * layer_bytes)
+    for l in range(LAYERS):
+        dev.fill_normal(routers, rh.DT_BF16, E * D, SEED, 16 + 16 * l + 8, scale=W_SCALE, byte_offset=l * E * D * esz)
+        dev.fill_normal(experts, rh.DT_BF16, layer_bytes // esz, SEED, (1 << 33) | l, scale=W_SCALE,
+                        byte_offset=l * layer_bytes)
+    xraw = dev.malloc(NX * D * 2)
+    dev.fill_normal(xraw, rh.DT_BF16, NX * D, SEED, 0x5EED)
+    xs = (dev.d2h(xraw, (NX * D,), np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(NX, D)
+    xb = dev.upload_array(xs)
+    layers = [rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers.offset(l * E * D * esz),
+                                experts.offset(l * layer_bytes), stride) for l in range(LAYERS)]
+    moe_out = dev.malloc(LAYERS * D * 4)
+    dev.reserve(layers[0], 1)
+    dev.set_router_order(rh.ORDER_AVX2)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        for l in range(LAYERS):
+            i = (s * LAYERS + l) % NX
+            dev.moe_dev(layers[l], xb.offset(i * D * 4), 1, moe=moe_out.offset(l * D * 4))
+    dev.synchronize()
+    print(f"profile-decode: {steps} eager steps of the 16-layer MoE stack in {time.perf_counter() - t0:.3f} s",
+          file=sys.stderr, flush=True)
     dev.close()
 
 
