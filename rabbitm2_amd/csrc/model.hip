@@ -537,13 +537,29 @@ __device__ __forceinline__ void attn_g8_load(f32x4 (&kr)[4], f32x4 (&vr)[4], con
     }
 }
 
+// With one split (S = 1) the block writes the attention output itself: what attn_merge_kernel computes
+// for a single partial (weight exp(0) = 1, sum L), into ao [B][q_dim] and, if given, the matrix-core planes.
+__device__ __forceinline__ void attn_out_direct(float *ao, uint16_t *ao_hi, uint16_t *ao_lo, int b, int B, int h,
+                                                int hd, int q_dim, int i, float acc, float L) {
+    const float v = (0.0f + acc) * (1.0f / L);
+    ao[(size_t)b * q_dim + (size_t)h * hd + i] = v;
+    if (ao_hi) {
+        const size_t oi = mfma_plane_index(b, h * hd + i, (B + 15) / 16);
+        const uint32_t hb = f32_to_bf16_rne(v);
+        ao_hi[oi] = (uint16_t)hb;
+        ao_lo[oi] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(hb << 16));
+    }
+}
+
 template <int AE>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_raw, const float *__restrict__ k_raw,
                                                    const float *__restrict__ v_raw, const float *__restrict__ qw,
                                                    const float *__restrict__ kw, int qk_norm, float eps, int n_heads,
                                                    int n_kv, int hd, int S, const StepState *__restrict__ st,
                                                    float *__restrict__ kc, float *__restrict__ vc, size_t seq_stride,
-                                                   const float2 *__restrict__ rope_cs, float *__restrict__ part) {
+                                                   const float2 *__restrict__ rope_cs, float *__restrict__ part,
+                                                   float *__restrict__ ao, uint16_t *__restrict__ ao_hi,
+                                                   uint16_t *__restrict__ ao_lo) {
     __shared__ __align__(16) float qh[256], kh[256], vh[256];
     __shared__ float red[16], w_m[4], w_l[4];
     __shared__ __align__(16) float w_o[4][256];
@@ -686,7 +702,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
             step(kb, vb, tn);
         }
         // merge the 32 (wave, group) partials: scales by wave 0, then one element per thread
-        __shared__ float g_m[32], g_l[32], g_a[32];
+        __shared__ float g_m[32], g_l[32], g_a[32], g_L;
         __shared__ __align__(16) float g_o[32][kAttnG8Hd];
         const int src = wv * 8 + g;
         if (j == 0) {
@@ -704,8 +720,11 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
             if (lane < 32) g_a[lane] = a;
             const float L = wave_sum(a * ls);
             if (lane == 0) {
-                po[0] = M;
-                po[1] = L;
+                g_L = L;
+                if (!ao) {
+                    po[0] = M;
+                    po[1] = L;
+                }
             }
         }
         __syncthreads();
@@ -713,7 +732,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
             float acc = 0.0f;
 #pragma unroll 8
             for (int q2 = 0; q2 < 32; ++q2) acc += g_a[q2] * g_o[q2][tid];
-            po[2 + tid] = acc;
+            if (ao)
+                attn_out_direct(ao, ao_hi, ao_lo, b, gridDim.z, h, hd, n_heads * hd, tid, acc, g_L);
+            else
+                po[2 + tid] = acc;
         }
         return;
     }
@@ -793,9 +815,14 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
         sw[w] = w_l[w] > 0.0f ? expf(w_m[w] - M) : 0.0f;
         L += sw[w] * w_l[w];
     }
-    for (int i = tid; i < hd; i += blockDim.x)
-        po[2 + i] = ((sw[0] * w_o[0][i] + sw[1] * w_o[1][i]) + (sw[2] * w_o[2][i] + sw[3] * w_o[3][i]));
-    if (tid == 0) {
+    for (int i = tid; i < hd; i += blockDim.x) {
+        const float acc = ((sw[0] * w_o[0][i] + sw[1] * w_o[1][i]) + (sw[2] * w_o[2][i] + sw[3] * w_o[3][i]));
+        if (ao)
+            attn_out_direct(ao, ao_hi, ao_lo, b, gridDim.z, h, hd, n_heads * hd, i, acc, L);
+        else
+            po[2 + i] = acc;
+    }
+    if (tid == 0 && !ao) {
         po[0] = M;
         po[1] = L;
     }
@@ -1370,21 +1397,23 @@ hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
-                            float *part, int B) {
+                            float *part, int B, float *ao, uint16_t *ao_hi, uint16_t *ao_lo) {
     if (hd > kWave * kAttnMaxE || S > 64) return hipErrorInvalidValue;
+    if (ao && (S != 1 || (ao_hi == nullptr) != (ao_lo == nullptr) || (ao_hi && (B > 64 || (n_heads * hd) % 32 != 0))))
+        return hipErrorInvalidValue;
     const dim3 g((unsigned)n_heads, (unsigned)S, (unsigned)B), b(256);
     const int kvd = n_kv * hd;
     if (hd == kAttnG8Hd && kvd % 4 == 0 && seq_stride % 4 == 0 && al16(kc) && al16(vc))
         return launch(L, attn_kernel<0>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                      seq_stride, rope_cs, part);
+                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
     if (hd <= kWave)
         return launch(L, attn_kernel<1>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                      seq_stride, rope_cs, part);
+                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
     if (hd <= 2 * kWave)
         return launch(L, attn_kernel<2>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                      seq_stride, rope_cs, part);
+                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
     return launch(L, attn_kernel<kAttnMaxE>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                  seq_stride, rope_cs, part);
+                  seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
 }
 
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,

@@ -111,6 +111,8 @@ hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype
 // threads; at 32 tokens 5.0 us against 19.9 us for the batch kernel, and with the top-k + split launch
 // 9.7 us against 18.1 us for the fused prefill front end; at 512 tokens 28.2 + 4.7 against 19.5 us).
 constexpr int kRouterDecodeMaxT = 64;
+// (sequence, head) attention blocks from which a step takes one position split (no merge launch).
+constexpr int kAttnDirectBlocks = 512;
 // Softmax + top-k of T tokens' logits [T][E] (E <= 64) and the bf16 hi/lo split of their rows xb [T][D]
 // (D % 8 == 0, 16-byte aligned) into x_hi / x_lo [T][D]: one block per token.
 hipError_t launch_topk_split(const Launch &L, const float *logits, int T, int E, int K, int norm_topk, const float *xb,
@@ -209,13 +211,16 @@ hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const
                                const void *W, int rows, float *logits, float2 *cand, StepState *st, int32_t *seq,
                                int ctx);
 // Attention of one step: grid (n_heads, S splits of the positions), each block writes its partial
-// (m, l, o[hd]) to part [n_heads][S][hd + 2]; launch_attn_merge merges them into ao (S <= 64).
+// (m, l, o[hd]) to part [n_heads][S][hd + 2]; launch_attn_merge merges them into ao (S <= 64). With
+// S == 1 and ao given, the attention writes ao [B][n_heads * hd] (and the matrix-core planes ao_hi /
+// ao_lo, if given) itself, bit for bit what the merge would, and no merge is launched.
 // rope_cs: [ctx][hd/2] (cos, sin) of the engine's RoPE angles. hd <= 256.
 // kc/vc: this layer's cache of sequence 0; sequence b's starts seq_stride floats further.
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
-                            float *part, int B);
+                            float *part, int B,
+                            float *ao = nullptr, uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr);
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,
                              uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr);
 // Dense rows over B token vectors xin [B][D] (batched decode): out_s [B][rows_s], or with resid != NULL
