@@ -343,7 +343,7 @@ int model_alloc(rbt_hip *h) {
 // the logits), top-k + the activation split, then dispatch, the grouped GEMMs and the combine into x
 // (rabbit2.c:512-542 for each token).
 int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float eps, int T, float *x, float *xb,
-                     int32_t *routing) {
+                     int32_t *routing, const float *next_nw, uint16_t *next_hi, uint16_t *next_lo) {
     if (!ws_reserve(h, T, L->n_experts, L->top_k, L->expert_hidden)) return 0;
     if (!pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim))) return 0;
     Workspace &w = h->ws;
@@ -356,9 +356,35 @@ int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float 
     int32_t *counts = nullptr;
     HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
                              L->experts, L->expert_stride, xb, T, L->n_experts, L->top_k, L->dim, L->expert_hidden,
-                             routing, w.weights, w.hbuf, w.pre, x, nullptr, &counts, true));
+                             routing, w.weights, w.hbuf, w.pre, x, nullptr, &counts, true, next_nw == nullptr));
     h->expert_counts = counts;
+    if (next_nw) {  // the combine, fused with the RMSNorm the next step starts with (xb and its planes)
+        const float *y = nullptr;
+        const int32_t *pos_of = nullptr;
+        prefill_combine_inputs(w.pre, T, L->n_experts, L->top_k, L->dim, &y, &pos_of);
+        HIP_OK(h, launch_combine_rmsnorm(lc(h, kProfCombine), y, pos_of, w.weights, L->top_k, T, L->dim, x, next_nw,
+                                         eps, xb, next_hi, next_lo));
+    }
     return prof_collect(h);
+}
+
+// Whether the batched step's q/k/v of layer l (and its lm_head) run on the matrix cores behind an
+// RMSNorm launch that writes the planes (the branches of enqueue_step below).
+bool qkv_mfma(const rbt_hip *h, int l, int B) {
+    const rbt_config &c = h->cfg;
+    const LayerOff &ly = h->layers[(size_t)l];
+    const int qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const void *W[3] = {h->model + ly.wq, h->model + ly.wk, h->model + ly.wv};
+    const int rows[3] = {qd, kvd, kvd};
+    return B > 1 && dense_supported(c.dtype, c.dim, W, rows) && h->batch_mfma &&
+           dense_mfma_supported(c.dtype, B, c.dim, W, rows);
+}
+bool lm_head_mfma(const rbt_hip *h, int B) {
+    const rbt_config &c = h->cfg;
+    const void *W[3] = {h->model + h->lm_head, nullptr, nullptr};
+    const int rows[3] = {c.vocab, 0, 0};
+    return B > 1 && dense_supported(c.dtype, c.dim, W, rows) && h->batch_mfma &&
+           dense_mfma_supported(c.dtype, B, c.dim, W, rows);
 }
 
 int enqueue_step(rbt_hip *h, bool final) {
@@ -375,7 +401,10 @@ int enqueue_step(rbt_hip *h, bool final) {
         if (!prof_collect(h)) return 0;       \
     } while (0)
     STEP_LAUNCH(kProfEmbed, launch_embed(L, c.dtype, h->model + h->tok_emb, D, c.vocab, ds.st, ds.seq, ds.ctx, ds.x, B));
+    bool xb_ready = false;  // the previous MoE block's combine already wrote xb and its planes
     for (int l = 0; l < c.n_layers; l++) {
+        const bool have_xb = xb_ready;  // for this layer's q/k/v only
+        xb_ready = false;
         const LayerOff &ly = h->layers[(size_t)l];
         const void *W[3] = {h->model + ly.wq, h->model + ly.wk, h->model + ly.wv};
         float *const out[3] = {ds.q, ds.k, ds.v};
@@ -384,9 +413,10 @@ int enqueue_step(rbt_hip *h, bool final) {
         const bool dense = dense_supported(c.dtype, D, W, rows);
         if (B == 1 && dense) {
             STEP_LAUNCH(kProfQkv, launch_dense_norm(L, c.dtype, ds.x, attn_norm, c.rms_eps, D, W, out, rows));
-        } else if (dense && h->batch_mfma && dense_mfma_supported(c.dtype, B, D, W, rows)) {
+        } else if (qkv_mfma(h, l, B)) {
             // batched on the matrix cores: the norm also writes the bf16 hi/lo planes of xb
-            STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl));
+            if (!have_xb)
+                STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl));
             STEP_LAUNCH(kProfQkv, launch_dense_mfma(L, ds.xh, ds.xl, B, D, W, out, rows, nullptr));
         } else if (dense) {  // batched: the norm once per token, then every weight read once for all tokens
             STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, attn_norm, D, c.rms_eps, ds.xb, B));
@@ -446,7 +476,16 @@ int enqueue_step(rbt_hip *h, bool final) {
                    router_norm_supported(h->order, c.dtype, B, D, ml.router, ds.x, ffn_norm) &&
                    prefill_supported(c.dtype, B, h->prefill_min_tokens, c.n_experts, c.top_k, D, c.expert_hidden,
                                      ml.experts, ml.expert_stride, ds.xb)) {
-            if (!moe_grouped_norm(h, &ml, ffn_norm, c.rms_eps, B, ds.x, ds.xb, routing)) return 0;
+            // the next step's first RMSNorm (next layer's q/k/v, or the lm_head) fused into the combine
+            const float *next_nw = nullptr;
+            if (l + 1 < c.n_layers && qkv_mfma(h, l + 1, B))
+                next_nw = reinterpret_cast<const float *>(h->model + h->layers[(size_t)l + 1].attn_norm);
+            else if (l + 1 == c.n_layers && final && lm_head_mfma(h, B))
+                next_nw = reinterpret_cast<const float *>(h->model + h->final_norm);
+            if (!moe_grouped_norm(h, &ml, ffn_norm, c.rms_eps, B, ds.x, ds.xb, routing, next_nw,
+                                  next_nw ? ds.xh : nullptr, next_nw ? ds.xl : nullptr))
+                return 0;
+            xb_ready = next_nw != nullptr;
         } else {
             STEP_LAUNCH(kProfFfnNorm, launch_rmsnorm(L, ds.x, ffn_norm, D, c.rms_eps, ds.xb, B));
             if (!rbt_hip_moe_dev(h, &ml, ds.xb, B, ds.x, nullptr, routing, nullptr)) return 0;
@@ -465,8 +504,9 @@ int enqueue_step(rbt_hip *h, bool final) {
         } else {
             if (dense && B == 1) {
                 STEP_LAUNCH(kProfLmHead, launch_dense_norm(L, c.dtype, ds.x, fn, c.rms_eps, D, W, out, rows));
-            } else if (dense && h->batch_mfma && dense_mfma_supported(c.dtype, B, D, W, rows)) {
-                STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl));
+            } else if (lm_head_mfma(h, B)) {
+                if (!xb_ready)
+                    STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B, ds.xh, ds.xl));
                 STEP_LAUNCH(kProfLmHead, launch_dense_mfma(L, ds.xh, ds.xl, B, D, W, out, rows, nullptr));
             } else if (dense) {
                 STEP_LAUNCH(kProfAttnNorm, launch_rmsnorm(L, ds.x, fn, D, c.rms_eps, ds.xb, B));

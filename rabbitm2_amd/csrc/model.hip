@@ -931,6 +931,69 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float *__restrict__
     for (int i = threadIdx.x + 1024 * U; i < n; i += blockDim.x) put(i, x[i] * inv * w[i]);
 }
 
+// The grouped path's combine for token t (combine_rows_kernel's arithmetic: moe = sum_k w_k y[pos(t,k)]
+// in selection order with rounded products, x += moe, rabbit2.c:540-542) followed by rmsnorm_kernel on
+// the new row (same per-thread order and block sum, same planes): one block per token, n <= 4096, K <= 8.
+__global__ __launch_bounds__(1024) void combine_rmsnorm_kernel(const float *__restrict__ y,
+                                                               const int32_t *__restrict__ pos_of,
+                                                               const float *__restrict__ weights, int K, int n,
+                                                               float *__restrict__ x, const float *__restrict__ w,
+                                                               float eps, float *__restrict__ out,
+                                                               uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
+    __shared__ float red[16];
+    const int t = blockIdx.x;
+    x += (size_t)t * n;
+    out += (size_t)t * n;
+    const int tbs = (gridDim.x + 15) / 16;
+    int p[8];
+    float wk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int kc = min(k, K - 1);
+        p[k] = pos_of[t * K + kc];
+        wk[k] = weights[t * K + kc];
+    }
+    constexpr int U = 4;
+    float xr[U], wr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = min((int)threadIdx.x + 1024 * u, n - 1);
+        float tmp[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) tmp[k] = y[(size_t)p[k] * n + i];
+        float moe = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+#pragma clang fp contract(off)
+            if (k < K) moe = moe + wk[k] * tmp[k];
+        }
+        xr[u] = x[i] + moe;
+        wr[u] = w[i];
+    }
+    float ss = 0.0f;  // rmsnorm_kernel's per-thread order
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if ((int)threadIdx.x + 1024 * u < n) ss += xr[u] * xr[u];
+    ss = block_sum(ss, red);  // its first barrier also orders every read of x before the stores below
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if ((int)threadIdx.x + 1024 * u < n) x[threadIdx.x + 1024 * u] = xr[u];
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = threadIdx.x + 1024 * u;
+        if (i >= n) continue;
+        const float v = xr[u] * inv * wr[u];
+        out[i] = v;
+        if (hi) {
+            const size_t pi = mfma_plane_index(t, i, tbs);
+            const uint32_t h = f32_to_bf16_rne(v);
+            hi[pi] = (uint16_t)h;
+            lo[pi] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(h << 16));
+        }
+    }
+}
+
 // ---------------------------------------------------------------- greedy argmax (rabbit2.c:552-556)
 // best = 0; for i: if v[i] > v[best] best = i -- the first index of the largest value; a NaN never
 // wins, and a NaN at index 0 is never beaten. Then the step advances: seq[pos + 1] = best when that
@@ -1434,6 +1497,17 @@ hipError_t launch_wo(const Launch &L, int dtype, const float *ao, int q_dim, con
                    : launch(L, wo_kernel<RBT_DT_BF16, false>, g, b, lds, ao, q_dim, W, D, x);
     return vec ? launch(L, wo_kernel<RBT_DT_F32, true>, g, b, lds, ao, q_dim, W, D, x)
                : launch(L, wo_kernel<RBT_DT_F32, false>, g, b, lds, ao, q_dim, W, D, x);
+}
+
+hipError_t launch_combine_rmsnorm(const Launch &L, const float *y, const int32_t *pos_of, const float *weights, int K,
+                                  int T, int n, float *x, const float *w, float eps, float *out, uint16_t *hi,
+                                  uint16_t *lo) {
+    if (T <= 0) return hipSuccess;
+    if (K < 1 || K > 8 || n < 1 || n > 4096 || T > 65535 || (hi == nullptr) != (lo == nullptr) ||
+        (hi && (T > 64 || n % 32 != 0)))
+        return hipErrorInvalidValue;
+    return launch(L, combine_rmsnorm_kernel, dim3((unsigned)T), dim3(1024), 0, y, pos_of, weights, K, n, x, w, eps, out,
+                  hi, lo);
 }
 
 hipError_t launch_rmsnorm(const Launch &L, const float *x, const float *w, int n, float eps, float *out, int B,

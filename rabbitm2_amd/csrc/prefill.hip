@@ -473,6 +473,12 @@ PrefillWs carve_ws(void *ws, int T, int E, int K, int D) {
 }
 }  // namespace
 
+void prefill_combine_inputs(void *ws, int T, int E, int K, int D, const float **y, const int32_t **pos_of) {
+    const PrefillWs r = carve_ws(ws, T, E, K, D);
+    *y = r.y;
+    *pos_of = r.pos_of;
+}
+
 void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uint16_t **x_lo) {
     const PrefillWs r = carve_ws(ws, T, E, K, D);
     *x_hi = r.x_hi;
@@ -482,7 +488,7 @@ void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uin
 hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
-                          int32_t **counts_out, bool x_split_done) {
+                          int32_t **counts_out, bool x_split_done, bool combine) {
     const int P = T * K;
     const PrefillWs r = carve_ws(ws, T, E, K, D);
     int32_t *counts = r.counts, *offsets = r.offsets, *m_off = r.m_off, *perm = r.perm, *pos_of = r.pos_of;
@@ -525,6 +531,7 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
               : launch_gemm<1, 64>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts,
                                    offsets, m_off, E, max_mtiles, y, nullptr, nullptr);
     if (e != hipSuccess) return e;
+    if (!combine) return hipSuccess;
     return launch(Lc, combine_rows_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)T), dim3(256), 0,
                   (const float *)y, (const int32_t *)pos_of, weights, K, D, x_inout, moe_out);
 }

@@ -160,8 +160,18 @@ size_t prefill_workspace_bytes(int T, int E, int K, int D);
 hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
-                          int32_t **counts_out, bool x_split_done);
+                          int32_t **counts_out, bool x_split_done,
+                          bool combine = true);
 void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uint16_t **x_lo);
+// combine = false: launch_prefill stops after the down GEMM; the combine's inputs (y [P][D] in list
+// order, pos_of [P]) are then these, for launch_combine_rmsnorm.
+void prefill_combine_inputs(void *ws, int T, int E, int K, int D, const float **y, const int32_t **pos_of);
+// The grouped path's combine (x += sum_k w[t][k] y[pos_of[t*K+k]] in selection order, K <= 8) fused
+// with the RMSNorm of the new rows that the next step starts with (out = x * inv * w, and the
+// matrix-core planes if hi/lo are given): one block per token, bit for bit the two launches.
+hipError_t launch_combine_rmsnorm(const Launch &L, const float *y, const int32_t *pos_of, const float *weights, int K,
+                                  int T, int n, float *x, const float *w, float eps, float *out, uint16_t *hi,
+                                  uint16_t *lo);
 
 // Router logits + softmax + top-k + the activation hi/lo split in one launch, for the grouped path
 // (AVX2 order, E <= 64). x_hi/x_lo may be NULL (no split).
