@@ -200,7 +200,9 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
  * lists -- and "combine", and its "down_combine" is the down GEMM alone); rbt_hip_forward adds
  * "embed", "attn_norm", "qkv" (RMSNorm + q/k/v), "attention", "attn_merge", "wo", "ffn_norm",
  * "lm_head" (final norm + lm_head, with the argmax inside where the rows allow) and "argmax"
- * (otherwise). rbt_hip_generate is never timed this way. Modes (on):
+ * (otherwise). Batched steps launch fewer: from 512 (sequence, head) pairs the attention writes its
+ * output without "attn_merge", and on the grouped path "combine" also runs the RMSNorm that the
+ * next step would time as "attn_norm". rbt_hip_generate is never timed this way. Modes (on):
  *   0  off.
  *   1  each call waits for its own kernels and adds their durations (eager calls only).
  *   2  deferred: each launch takes a fresh event pair and nothing waits, so timed calls run back
