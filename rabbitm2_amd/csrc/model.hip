@@ -1322,7 +1322,8 @@ bool dense_mfma_supported(int dtype, int B, int K, const void *const W[3], const
 namespace {
 // Row tiles below which a product over two or more token blocks is split by token block: fewer tiles
 // than CUs leave CUs idle (wo at 2048 rows, 128 tiles: 7.7 -> 6.6 us at 32 tokens), while more have
-// each weight row read twice (q/k/v at 6144 rows, 384 tiles: 14.2 -> 16.6 us when split).
+// each weight row read twice (q/k/v at 6144 rows, 384 tiles: 14.2 -> 16.6 us when split, 15.5 us even
+// with a tile's token blocks placed 8 blocks apart, on one XCD back to back, to share its L2).
 constexpr int kMfmaSplitTiles = 256;
 template <int KS, int MODE>
 hipError_t dense_mfma_ks(const Launch &L, const uint16_t *xh, const uint16_t *xl, int B, const Segs &sg,
