@@ -478,9 +478,10 @@ int enqueue_step(rbt_hip *h, bool final) {
                                      ml.experts, ml.expert_stride, ds.xb)) {
             // the next step's first RMSNorm (next layer's q/k/v, or the lm_head) fused into the combine
             const float *next_nw = nullptr;
-            if (l + 1 < c.n_layers && qkv_mfma(h, l + 1, B))
+            const bool fusable = c.top_k <= 8 && D <= 4096;  // launch_combine_rmsnorm's limits
+            if (fusable && l + 1 < c.n_layers && qkv_mfma(h, l + 1, B))
                 next_nw = reinterpret_cast<const float *>(h->model + h->layers[(size_t)l + 1].attn_norm);
-            else if (l + 1 == c.n_layers && final && lm_head_mfma(h, B))
+            else if (fusable && l + 1 == c.n_layers && final && lm_head_mfma(h, B))
                 next_nw = reinterpret_cast<const float *>(h->model + h->final_norm);
             if (!moe_grouped_norm(h, &ml, ffn_norm, c.rms_eps, B, ds.x, ds.xb, routing, next_nw,
                                   next_nw ? ds.xh : nullptr, next_nw ? ds.xl : nullptr))

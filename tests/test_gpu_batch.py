@@ -151,6 +151,30 @@ def test_forward_batch_grouped_front_end_renormalised(dev):
             assert normwise_err(logits[b], wl[p]) <= LOGIT_RTOL, f"seq {b} pos {p}"
 
 
+def test_forward_batch_grouped_top10_of_16(dev):
+    """The grouped MoE path of the batched forward with more than 8 selected experts (16 experts,
+    top-10): the per-token top-k launch, the combine's general loop and a separate RMSNorm launch
+    (the fused combine + RMSNorm takes at most 8), against the oracle on each sequence alone."""
+    spec = MANIFEST["cases"]["tiny_olmoe_bf16"]
+    cfg = po.Config(**dict(spec["config"], n_experts=16, top_k=10))
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"] + 3, w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    B, n = 16, 3
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, n, seed=23)
+    want = [po.run(model, prompts[b], order=po.ORDER_AVX2) for b in range(B)]
+    dev.batch_init(B, 0)
+    for p in range(n):
+        logits, routing = dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
+                                            cfg.top_k)
+        for b in range(B):
+            wl, wr, _ = want[b]
+            assert np.array_equal(routing[:, b, :], wr[p]), f"seq {b} pos {p}"
+            assert normwise_err(logits[b], wl[p]) <= LOGIT_RTOL, f"seq {b} pos {p}"
+
+
 def test_forward_batch_sequences_restart_independently(dev):
     """Sequence 1 starts over at position 0 every 3 steps while sequence 0 runs on: each is its own
     forward() stream (a restart overwrites only that sequence's cache)."""
