@@ -2,7 +2,7 @@
 
 ctypes view of liboracle.so (the CPU restatement of the RABBIT2 engine arithmetic, see
 rbt2_oracle.h). Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import this,
-always as the checker; the product library never does.
+only to check results or to time the CPU baseline; the product library never does.
 """
 import ctypes as C
 import os

@@ -2,7 +2,7 @@
  * ORACLE -- test infrastructure, not product code.
  *
  * A CPU restatement of the RABBIT2 engine's arithmetic (rabbit2/src/rabbit2.c) and of its .rbt2
- * storage format (rabbit2/ref/rbt2.py). It is the checker for the HIP path: only the test suite,
+ * storage format (rabbit2/ref/rbt2.py). It checks the HIP path's results: only the test suite,
  * the smoke check and the CPU-baseline leg of the benchmark load it. The product library never
  * links, loads or calls anything here.
  *
