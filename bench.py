@@ -113,7 +113,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+        print(f"bench.py: the MoE-layer path runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
               "multi-GPU sharding of the MoE layer is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
 
