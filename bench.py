@@ -1,24 +1,29 @@
-"""Benchmark of the MI355X MoE-layer path at the OLMoE-1B-7B shape, batch-1 decode.
+"""Benchmark of the MI355X path for the RABBIT2 engine at the OLMoE-1B-7B shape.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 
-Workload: one step = one decode token through the 16 MoE layers of an OLMoE-1B-7B-shaped model
-(each layer: hidden 2048, 64 experts, top-8, SwiGLU intermediate 1024, bf16 weights ~N(0, 0.02),
-renormalised top-8 weights). All 16 layers' routers and experts (12.9 GB) are resident in HBM in
-the .rbt2 storage format; every layer reads its own weights, so a step streams ~1.6 GB and the
-256 MB last-level cache cannot hold a step's working set. Inputs are bf16-valued N(0,1)
-activations already in HBM; each (step, layer) takes one of 64 pre-generated vectors, so the
-selected experts change from step to step. Only the MoE blocks are timed (the attention half of
-the model is not part of this path).
+Headline ("value"): batch-1 greedy decode of the whole OLMoE-1B-7B-shaped random-init model -- 16
+layers, hidden 2048, 16 heads x 128 with QK-norm and RoPE, 64 experts top-8, SwiGLU 1024, vocab 50304,
+bf16 weights ~N(0, 0.02), f32 KV cache in HBM -- on a 128-token random prompt, through the device-side
+--gen loop (one HIP graph replay per token, the argmax on the device feeding the next step). One step =
+one token's forward() + final norm + lm_head + argmax. W untimed steps, then a fresh run of the prompt
+and K + 1 generated tokens whose K steps after the first are timed with HIP events on the library's
+stream (default K = 255: the 256 generated tokens of the workload). value = K / their time.
 
-Prints one JSON line: tok/s of the 16-layer MoE stack; the roofline of the dominant kernel
-(expert gate/up GEMV) from HIP events on the stream it runs on; the whole-layer HBM rate; the
-512-token prefill of layer 0 ("prefill": uniform and skewed routing, tokens-per-expert histogram,
-HBM rate and matrix-core utilisation of the grouped GEMMs); the whole OLMoE-1B-7B-shaped model
-("full_model": 16 layers with attention, vocab 50304, a 128-token prompt and 256 greedy tokens
-through the device-side generate loop, and "batched_decode": 32 sequences with 2048-token contexts, 64
-greedy tokens each); and the CPU baselines (the oracle, the engine's own
-arithmetic in its AVX2 order, on one host core).
+The same JSON line carries:
+  roofline  the dominant kernel of that step (the MoE gate/up kernel: softmax + top-k, the 8 selected
+            experts' w1/w3 rows, SwiGLU): algorithmic bytes / its average duration, from HIP events
+            around every launch in eager forward() steps at the generated positions; traffic from the
+            calibrated rocprofv3 counter runs kept under profiles/.
+  layer     the MoE layer alone (the metric's "MoE-layer HBM GB/s & % of peak"): 16 OLMoE-shaped MoE
+            layers with renormalised top-8, one token per step, each layer reading its own 100.9 MB,
+            replayed from a HIP graph; per-layer time, HBM rate, per-kernel times; the host-pointer
+            seam rbt_hip_moe's per-call cost.
+  full_model  per-kernel times of the decode step, prompt rate, bytes per token; batched_decode (32
+            sequences with 2048-token contexts, 64 greedy tokens each).
+  prefill   512 tokens through one layer, uniform and skewed routing (histogram, HBM rate, MFMA use).
+  cpu_baseline  the oracle's forward() (the engine's own arithmetic, AVX2 order, bitwise the
+            reference binary) on one host core over a bounded prefix of the same prompt.
 """
 import argparse
 import ctypes as C
@@ -38,9 +43,12 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 D, E, K, H, LAYERS = 2048, 64, 8, 1024, 16
 SEED = 1
 W_SCALE = 0.02
-NX = 64  # distinct input vectors cycled through
+NX = 64  # distinct input vectors cycled through by the MoE-layer leg
 TRAFFIC_KEY = {"gateup": "gateup_fast"}
 KERNEL_DESC = {"gateup": "gateup_fast (softmax + top-k, expert gate+up projections, SwiGLU)"}
+STEP_KERNELS = ("embed", "qkv", "attention", "attn_merge", "wo", "router", "gateup", "down_combine", "lm_head",
+                "argmax")
+PROFILE_STEPS = 32  # eager forward() steps timed per kernel after the timed run
 
 
 def hip_events():
@@ -82,20 +90,31 @@ def cpu_model():
     return "unknown"
 
 
+def step_bytes(cfg, pos):
+    """Algorithmic HBM bytes of one decode step at position pos: every dense weight once, the router and
+    the 8 selected experts of every layer, the lm_head, and the f32 K/V rows of positions 0..pos."""
+    D_, hd = cfg.dim, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    esz = 2
+    per_layer = (qd + 2 * kvd) * D_ * esz + D_ * qd * esz + cfg.n_experts * D_ * esz + \
+        cfg.top_k * 3 * cfg.expert_hidden * D_ * esz
+    return cfg.n_layers * per_layer + cfg.vocab * D_ * esz + D_ * esz + cfg.n_layers * 2 * kvd * 4 * (pos + 1)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-fused", action="store_true", help="separate top-k launch (four launches per layer) "
-                    "instead of the top-k inside the gate/up kernel")
-    ap.add_argument("--eager", action="store_true", help="launch every layer from Python instead of replaying a "
-                    "captured HIP graph of the steps")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target length of the CPU baseline sample")
+    ap.add_argument("--steps", type=int, default=N_GEN - 1, help="timed decode steps (default: the 255 steps "
+                    "after the first of the workload's 256 generated tokens)")
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target length of each CPU baseline sample")
+    ap.add_argument("--layer-steps", type=int, default=200, help="timed steps of the MoE-layer leg")
+    ap.add_argument("--no-layer", action="store_true", help="skip the MoE-layer (and prefill) legs")
+    ap.add_argument("--no-fused", action="store_true", help="MoE-layer leg: separate top-k launch (four launches "
+                    "per layer) instead of the top-k inside the gate/up kernel")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token prefill leg")
     ap.add_argument("--prefill-reps", type=int, default=20, help="timed calls per prefill workload")
-    ap.add_argument("--no-full-model", action="store_true", help="skip the whole-model generate leg")
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode leg")
     ap.add_argument("--profile-forward", type=int, default=0, metavar="N",
                     help="only run N eager forward() steps of the whole model (for kernel traces) and exit")
@@ -113,9 +132,11 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: the MoE-layer path runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "multi-GPU sharding of the MoE layer is a design note, not a measured path.", file=sys.stderr)
+        print(f"bench.py: this path runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "sharding the MoE layer over GPUs is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("bench.py: --steps must be >= 1 and --warmup >= 0")
 
     if args.profile_forward > 0:
         profile_forward(args.profile_forward, args.profile_batch)
@@ -130,6 +151,158 @@ def main():
     from rabbitm2_amd import hip as rh
 
     dev = rh.Device(0)
+    hipapi, mk, elapsed = hip_events()
+    if args.copy_calib_mib:
+        # one device-to-device copy of known size (the runtime's blit kernel reads and writes exactly
+        # this many bytes), for scaling the FETCH_SIZE / WRITE_SIZE counters of a --pmc run
+        nb = args.copy_calib_mib << 20
+        src, dst = dev.malloc(nb), dev.malloc(nb)
+        dev.memset(src, 1)
+        hipapi.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        assert hipapi.hipMemcpyAsync(dst.p, src.p, nb, 3, C.c_void_p(dev.stream)) == 0  # hipMemcpyDeviceToDevice
+        dev.synchronize()
+        dev.free(src)
+        dev.free(dst)
+
+    # ---- headline: whole-model bs=1 greedy decode
+    cfg, setup_s = make_full_model(dev)
+    dev.set_router_order(rh.ORDER_AVX2)
+    K_steps = args.steps
+    n_gen = K_steps + 1
+    ctx = N_PROMPT + max(n_gen, args.warmup + 1, PROFILE_STEPS + 1)
+    dev.state_init(ctx)
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, N_PROMPT).astype(np.int32)
+    warm = []
+    if args.warmup > 0:
+        warm, _ = dev.generate(prompt, args.warmup + 1)  # graph capture and first touch; untimed
+    w0 = time.perf_counter()
+    ids, (p_ms, g_ms) = dev.generate(prompt, n_gen)  # K timed steps: the forwards after the first token
+    wall = time.perf_counter() - w0
+    assert len(ids) == n_gen and all(0 <= t < cfg.vocab for t in ids)
+    assert ids[:len(warm)] == warm, "generate is not deterministic"
+    ms_per_step = g_ms / K_steps
+    value = K_steps / (g_ms * 1e-3)
+    mean_pos = N_PROMPT + (n_gen - 1) / 2.0
+    tok_bytes = step_bytes(cfg, mean_pos)
+
+    # ---- per-kernel durations of the step: HIP events around every launch (deferred profiling, nothing
+    # waits between launches) in eager forward() steps at the generated positions
+    dev.state_init(ctx)
+    seq = prompt.tolist() + ids
+    for pos in range(N_PROMPT):
+        dev.forward(seq[pos], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
+    dev.profile(2)
+    for pos in range(N_PROMPT, N_PROMPT + PROFILE_STEPS):
+        dev.forward(seq[pos], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
+    kern = {}
+    for name in STEP_KERNELS:
+        tot, n = dev.profile_get(name)
+        if n:
+            kern[name] = {"avg_us": round(1000.0 * tot / n, 3), "launches_per_step": n // PROFILE_STEPS}
+    dev.profile(0)
+    esz = 2
+    alg = {"gateup": K * 2 * H * D * esz + D * 4 + K * H * 4,  # the 8 experts' w1/w3 rows, x, h written
+           "down_combine": K * D * H * esz + K * H * 4 + D * 4,
+           "router": E * D * esz + D * 4 * 2,
+           "lm_head": cfg.vocab * D * esz + D * 4}
+    for name, b in alg.items():
+        if name in kern:
+            kern[name]["alg_bytes"] = b
+            kern[name]["GBps"] = round(b / (kern[name]["avg_us"] * 1e-6) / 1e9, 1)
+    dom = kern["gateup"]
+    dom_gbs = alg["gateup"] / (dom["avg_us"] * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "olmoe_moe_layer_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath))["per_launch"][TRAFFIC_KEY["gateup"]]["bytes"]
+        except (KeyError, ValueError):
+            traffic = None
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "OLMoE-1B-7B-shaped random-init model, batch-1 greedy decode: 16 layers, hidden 2048, 16 "
+                        "heads x 128 (QK-norm, RoPE), 64 experts top-8, SwiGLU 1024, vocab 50304, bf16 weights "
+                        "~N(0,0.02), f32 KV cache in HBM; 128-token random prompt, then 256 generated tokens "
+                        "(255 timed steps), one HIP graph replay per token",
+            "model": "OLMoE-1B-7B shape", "layers": cfg.n_layers, "dim": cfg.dim, "n_experts": cfg.n_experts,
+            "top_k": cfg.top_k, "expert_hidden": cfg.expert_hidden, "vocab": cfg.vocab, "weights": "bf16",
+            "activations": "f32", "router_order": "avx2 (bit-exact engine order)", "global_batch": 1,
+            "prompt_tokens": N_PROMPT, "generated_tokens": n_gen,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": KERNEL_DESC["gateup"],
+            "achieved": round(dom_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "traffic_source": "profiles/olmoe_moe_layer_traffic.json" if traffic else None,
+            "alg_bytes_per_launch": alg["gateup"],
+            "avg_launch_us": dom["avg_us"],
+            "timing": f"HIP events around each launch, {PROFILE_STEPS} eager decode steps x 16 layers",
+        },
+        "full_model": {
+            "bytes_per_token": int(tok_bytes),
+            "hbm_GBps_alg": round(tok_bytes * value / 1e9, 1),
+            "hbm_frac_alg": round(tok_bytes * value / 1e9 / HBM_PEAK_GBS, 4),
+            "prompt_tok_per_s": round(N_PROMPT / (p_ms * 1e-3), 2),
+            "step_kernels": kern,
+            "launch": "one HIP graph per token (embedding .. argmax)",
+            "wall_s": round(wall, 3),
+            "setup_s": round(setup_s, 2),
+        },
+    }
+
+    if not args.no_batched:
+        out["full_model"]["batched_decode"] = batched_leg(dev, cfg)
+    out["full_model"]["host_pointer_moe"] = host_pointer_moe(dev, cfg)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_full_model(dev, cfg, prompt, args.cpu_seconds)
+    dev.state_init(1)  # release the decode state before the layer legs
+    if not args.no_layer:
+        out["layer"] = moe_layer_leg(dev, args)
+    print(json.dumps(out), flush=True)
+    dev.close()
+
+
+def host_pointer_moe(dev, cfg, reps=200):
+    """Per-call cost of the host-pointer MoE seam rbt_hip_moe (the call an engine patch puts into
+    forward(): xb and x copied in, x and the routing copied back, one wait) on layer 0 of the model."""
+    rng = np.random.default_rng(SEED + 3)
+    res = {}
+    for T in (1, 512):
+        xb = rng.standard_normal((T, cfg.dim)).astype(np.float32)
+        x = rng.standard_normal((T, cfg.dim)).astype(np.float32)
+        n = reps if T == 1 else max(5, reps // 20)
+        for _ in range(3):
+            dev.moe(0, xb, x=x)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            dev.moe(0, xb, x=x)
+        res[f"T{T}_us_per_call"] = round(1e6 * (time.perf_counter() - t0) / n, 1)
+    res["note"] = "wall time per call through ctypes (a few us of Python included), host buffers pageable"
+    return res
+
+
+def moe_layer_leg(dev, args):
+    """The MoE layer alone: 16 OLMoE-shaped MoE layers (router + 64 experts each, renormalised top-8),
+    one token per step, every layer reading its own weights; a HIP graph of steps replayed."""
+    from rabbitm2_amd import hip as rh
+    hipapi, mk, elapsed = hip_events()
     esz = 2
     stride = (3 * H * D * esz + 4095) // 4096 * 4096
     layer_bytes = E * stride
@@ -167,162 +340,84 @@ def main():
             dev.moe_dev(layers[l], xb.offset(i * D * 4), 1, moe=moe_out.offset(l * D * 4),
                         routing=routing.offset(l * K * 4))
 
-    hipapi, mk, elapsed = hip_events()
     stream = C.c_void_p(dev.stream)
-    if args.copy_calib_mib:
-        # one device-to-device copy of known size (the runtime's blit kernel reads and writes exactly
-        # this many bytes), for scaling the FETCH_SIZE / WRITE_SIZE counters of a --pmc run
-        nb = args.copy_calib_mib << 20
-        src, dst = dev.malloc(nb), dev.malloc(nb)
-        dev.memset(src, 1)
-        hipapi.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
-        assert hipapi.hipMemcpyAsync(dst.p, src.p, nb, 3, stream) == 0  # hipMemcpyDeviceToDevice
-        dev.synchronize()
-        dev.free(src)
-        dev.free(dst)
     # A decode engine replays a captured graph per token; one graph here holds GRAPH_STEPS steps so
     # the 64 input vectors are all cycled through (kernels only: no memset/copy nodes).
     GRAPH_STEPS = NX // LAYERS
-    for s in range(args.warmup):
+    for s in range(20):
         step(s)
     step(GRAPH_STEPS - 1)
     dev.synchronize()
     eager_ref = dev.d2h(moe_out, (LAYERS, D), np.float32)  # eager output of the graph's last step
-    gexec = None
-    if not args.eager:
-        graph, gexec = C.c_void_p(), C.c_void_p()
-        assert hipapi.hipStreamBeginCapture(stream, 2) == 0  # hipStreamCaptureModeRelaxed
-        for s in range(GRAPH_STEPS):
-            step(s)
-        assert hipapi.hipStreamEndCapture(stream, C.byref(graph)) == 0
-        assert hipapi.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0) == 0
-        # every replay must reproduce the eager result of the same step
-        for r in range(3):
-            assert hipapi.hipGraphLaunch(gexec, stream) == 0
-            dev.synchronize()
-            got = dev.d2h(moe_out, (LAYERS, D), np.float32)
-            assert got.tobytes() == eager_ref.tobytes(), "graph replay differs from eager launch"
-
-    steps = args.steps
-    if gexec is not None:
-        steps = (args.steps + GRAPH_STEPS - 1) // GRAPH_STEPS * GRAPH_STEPS
+    graph, gexec = C.c_void_p(), C.c_void_p()
+    assert hipapi.hipStreamBeginCapture(stream, 2) == 0  # hipStreamCaptureModeRelaxed
+    for s in range(GRAPH_STEPS):
+        step(s)
+    assert hipapi.hipStreamEndCapture(stream, C.byref(graph)) == 0
+    assert hipapi.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0) == 0
+    # every replay must reproduce the eager result of the same step
+    for r in range(3):
+        assert hipapi.hipGraphLaunch(gexec, stream) == 0
+        dev.synchronize()
+        got = dev.d2h(moe_out, (LAYERS, D), np.float32)
+        assert got.tobytes() == eager_ref.tobytes(), "graph replay differs from eager launch"
+    steps = (args.layer_steps + GRAPH_STEPS - 1) // GRAPH_STEPS * GRAPH_STEPS
     ev0, ev1 = mk(), mk()
-    w0 = time.perf_counter()
     hipapi.hipEventRecord(ev0, stream)
-    if gexec is not None:
-        for _ in range(steps // GRAPH_STEPS):
-            hipapi.hipGraphLaunch(gexec, stream)
-    else:
-        for s in range(steps):
-            step(args.warmup + s)
+    for _ in range(steps // GRAPH_STEPS):
+        hipapi.hipGraphLaunch(gexec, stream)
     hipapi.hipEventRecord(ev1, stream)
     dev.synchronize()
-    wall = time.perf_counter() - w0
-    gpu_ms = elapsed(ev0, ev1)
-    ms_per_step = gpu_ms / steps
-    args.steps = steps
+    ms_per_step = elapsed(ev0, ev1) / steps
+    hipapi.hipGraphExecDestroy(gexec)
+    hipapi.hipGraphDestroy(graph)
 
-    # ---- per-kernel durations: HIP events around every launch on the library stream, taken in a
-    # pass of eager steps that run back to back (deferred profiling: no wait between calls)
+    # per-kernel durations: HIP events around every launch on the library stream, in a pass of eager
+    # steps that run back to back (deferred profiling: no wait between calls)
     kern = {}
     dev.profile(2)
-    nprof = max(10, min(args.steps, 50))
-    for s in range(nprof):
+    for s in range(50):
         step(s)
     for name in ("router", "topk", "gateup", "down_combine"):
         tot, n = dev.profile_get(name)
         if n:
             kern[name] = {"avg_us": 1000.0 * tot / n, "launches": n}
     dev.profile(0)
-
-    w_experts = K * 3 * H * D * esz  # the 8 selected experts' w1, w3, w2
     alg_bytes = {
         "router": E * D * esz + D * 4,
         "topk": E * 4 * 2 + K * 8,  # logits in, probabilities out, routing + weights out
         "gateup": K * 2 * H * D * esz + D * 4 + K * H * 4,  # weights + x read + h written
         "down_combine": K * D * H * esz + K * H * 4 + D * 4,
     }
-    layer_alg = E * D * esz + w_experts  # 100,925,440: router + 8 experts
+    layer_alg = E * D * esz + K * 3 * H * D * esz  # 100,925,440: router + 8 experts
     for name in kern:
         kern[name]["alg_bytes"] = alg_bytes[name]
         kern[name]["GBps"] = alg_bytes[name] / (kern[name]["avg_us"] * 1e-6) / 1e9
-    dom_name = "gateup"
-    dom = kern[dom_name]
     layer_us = 1000.0 * ms_per_step / LAYERS
     layer_gbs = layer_alg / (layer_us * 1e-6) / 1e9
-
-    # routing histogram sanity (the last step's selections)
     last_routing = dev.d2h(routing, (LAYERS, K), np.int32)
     assert np.all((last_routing >= 0) & (last_routing < E))
-
-    # HBM bytes per launch of the dominant kernel, from the calibrated rocprofv3 --pmc runs kept
-    # under profiles/ (counters cannot be read from inside this process)
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "olmoe_moe_layer_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            traffic = json.load(open(tpath))["per_launch"][TRAFFIC_KEY[dom_name]]["bytes"]
-        except (KeyError, ValueError):
-            traffic = None
-
-    value = 1000.0 / ms_per_step
-    out = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {
-            "workload": "OLMoE-1B-7B MoE stack decode, bs=1: 16 MoE layers (hidden 2048, 64 experts, top-8, "
-                        "SwiGLU 1024, bf16 weights ~N(0,0.02), renormalised top-8), one token per step, "
-                        "all experts HBM-resident",
-            "layers": LAYERS, "dim": D, "n_experts": E, "top_k": K, "expert_hidden": H, "weights": "bf16",
-            "activations": "f32 (bf16-valued N(0,1))", "router_order": "avx2 (bit-exact engine order)",
-            "global_batch": 1,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": KERNEL_DESC[dom_name],
-            "achieved": round(dom["GBps"], 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_source": "profiles/olmoe_moe_layer_traffic.json" if traffic else None,
-            "alg_bytes_per_launch": alg_bytes[dom_name],
-            "avg_launch_us": round(dom["avg_us"], 3),
-        },
-        "layer": {
-            "alg_bytes": layer_alg,
-            "us": round(layer_us, 3),
-            "GBps": round(layer_gbs, 1),
-            "frac_of_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
-        },
+    res = {
+        "workload": "OLMoE-1B-7B MoE layer decode, bs=1: 16 MoE layers (hidden 2048, 64 experts, top-8, SwiGLU "
+                    "1024, bf16 weights ~N(0,0.02), renormalised top-8), one bf16-valued N(0,1) token per step, "
+                    "all experts HBM-resident, HIP graph of 4 steps replayed",
+        "alg_bytes": layer_alg,
+        "us": round(layer_us, 3),
+        "GBps": round(layer_gbs, 1),
+        "frac_of_hbm_peak": round(layer_gbs / HBM_PEAK_GBS, 4),
+        "moe_stack_tok_per_s": round(1000.0 / ms_per_step, 2),
+        "steps": steps,
         "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in kern.items()},
-        "launch": "eager" if gexec is None else f"hip graph ({GRAPH_STEPS} steps per graph)",
-        "wall_s": round(wall, 3),
         "setup_s": round(fill_s, 2),
     }
-
     if not args.no_prefill:
-        out["prefill"] = prefill_leg(dev, routers, experts, stride, args.prefill_reps, not args.no_cpu)
-
+        res["prefill"] = prefill_leg(dev, routers, experts, stride, args.prefill_reps, not args.no_cpu)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(dev, routers, experts, stride, xs_host, args.cpu_seconds)
-
-    if not args.no_full_model:
-        out["full_model"] = full_model_leg(not args.no_cpu, args.cpu_seconds, not args.no_batched)
-
-    print(json.dumps(out), flush=True)
-    dev.close()
+        res["cpu_baseline"] = cpu_baseline(dev, routers, experts, stride, xs_host, args.cpu_seconds)
+    for b in (routers, experts, xb, xraw, moe_out, routing):
+        dev.free(b)
+    return res
 
 
 # The whole model at the OLMoE-1B-7B shape (16 layers, 16 heads x 128 with QK-norm and RoPE, 64
@@ -360,51 +455,6 @@ def make_full_model(dev):
     fill_tensor("lm_head", 0, rh.DT_BF16, W_SCALE, 0.0)
     dev.synchronize()
     return cfg, time.time() - t0
-
-
-def full_model_leg(with_cpu, cpu_seconds, batched=True):
-    """128 random prompt ids, then 256 greedy tokens through rbt_hip_generate (one HIP graph replay
-    per token, the argmax feeding the next step on the device). Reports generated tok/s, prompt tok/s
-    and the weight bytes streamed per generated token."""
-    from rabbitm2_amd import hip as rh
-    dev = rh.Device(0)
-    cfg, setup_s = make_full_model(dev)
-    dev.set_router_order(rh.ORDER_AVX2)
-    dev.state_init(N_PROMPT + N_GEN)
-    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, N_PROMPT).astype(np.int32)
-    ids0, _ = dev.generate(prompt, N_GEN)  # warm-up (graph capture, first touch)
-    ids, (p_ms, g_ms) = dev.generate(prompt, N_GEN)
-    assert ids == ids0, "generate is not deterministic"
-    assert len(ids) == N_GEN and all(0 <= t < cfg.vocab for t in ids)
-    D_, hd = cfg.dim, cfg.head_dim
-    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
-    esz = 2
-    per_layer = (qd + 2 * kvd) * D_ * esz + D_ * qd * esz + cfg.n_experts * D_ * esz + \
-        cfg.top_k * 3 * cfg.expert_hidden * D_ * esz
-    w_bytes = cfg.n_layers * per_layer + cfg.vocab * D_ * esz + D_ * esz
-    mean_pos = N_PROMPT + (N_GEN - 1) / 2.0
-    kv_bytes = cfg.n_layers * 2 * kvd * 4 * mean_pos
-    gen_tok_s = (N_GEN - 1) / (g_ms * 1e-3)
-    tok_bytes = w_bytes + kv_bytes
-    res = {
-        "workload": "OLMoE-1B-7B-shaped model (16 layers, hidden 2048, 16 heads x 128, QK-norm, RoPE, 64 experts "
-                    "top-8, SwiGLU 1024, vocab 50304, bf16 ~N(0,0.02)), 128-token random prompt, greedy decode of "
-                    "256 tokens at batch 1 with the KV cache in HBM",
-        "gen_tok_per_s": round(gen_tok_s, 2),
-        "ms_per_token": round(g_ms / (N_GEN - 1), 4),
-        "prompt_tok_per_s": round(N_PROMPT / (p_ms * 1e-3), 2),
-        "bytes_per_token": int(tok_bytes),
-        "hbm_GBps_alg": round(tok_bytes * gen_tok_s / 1e9, 1),
-        "hbm_frac_alg": round(tok_bytes * gen_tok_s / 1e9 / HBM_PEAK_GBS, 4),
-        "launch": "one HIP graph per token (embedding .. argmax, 7 launches per layer + 3)",
-        "setup_s": round(setup_s, 2),
-    }
-    if with_cpu:
-        res["cpu_baseline"] = cpu_full_model(dev, cfg, prompt, cpu_seconds)
-    if batched:
-        res["batched_decode"] = batched_leg(dev, cfg)
-    dev.close()
-    return res
 
 
 def profile_forward(steps, batch):
@@ -540,15 +590,21 @@ def batched_leg(dev, cfg):
     }
 
 
-def cpu_full_model(dev, cfg, prompt, seconds):
-    """The engine's forward() (the oracle's orc_run, AVX2 order, bitwise the reference) on one host
-    core over a prefix of the prompt, on the same weights read back from HBM."""
-    from oracle import pyoracle as po
+def read_model_image(dev, cfg):
+    """The device model image as the bytes of a .rbt2 file (the 68-byte header written in front)."""
     size = dev.tensor("lm_head")[0] + dev.tensor("lm_head")[1]
     img = np.empty(size, np.uint8)
     dev._check(dev.L.rbt_hip_d2h(dev.h, img.ctypes.data_as(C.c_void_p), dev.model_base, size))
     hdr = np.frombuffer(b"RBT2" + np.uint32(2).tobytes() + bytes(cfg), np.uint8)  # the .rbt2 header (68 bytes)
     img[:hdr.size] = hdr
+    return img
+
+
+def cpu_full_model(dev, cfg, prompt, seconds):
+    """The engine's forward() (the oracle's orc_run, AVX2 order, bitwise the reference) on one host
+    core over a prefix of the prompt, on the same weights read back from HBM."""
+    from oracle import pyoracle as po
+    img = read_model_image(dev, cfg)
     try:
         old = os.sched_getaffinity(0)
         os.sched_setaffinity(0, {sorted(old)[0]})

@@ -7,6 +7,10 @@
  * int 1 = ok / 0 = error (the engine's convention, e.g. load_model :199, forward :455), with the
  * message kept per handle (rbt_hip_last_error) and also printed to stderr like the engine does.
  *
+ * Failure paths: with the environment variable RBT_HIP_FAULT="<kind>[:<n>]" (kind malloc, launch, copy
+ * or sync) the n-th HIP call of that kind in the process is reported as failed without being made,
+ * so every entry point's 0 + message path can be exercised from the host.
+ *
  * Threading: a handle is used by one host thread at a time (the engine is single-threaded,
  * rabbit2/README.md:255). All device work of a handle runs in order on the handle's own HIP
  * stream. Calls ending in _dev take device pointers and are asynchronous on that stream; every
@@ -69,6 +73,9 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *                         q/k/v, wo and lm_head for up to 64 sequences on the matrix cores (bf16
  *                         weights; activations as bf16 hi + lo parts, exact products); 0: VALU dot
  *                         products. Both agree with the engine to rounding.
+ *   "routing_history"     0 (default) / 1: from the next rbt_hip_state_init / rbt_hip_batch_init on,
+ *                         every forward step also records its routing per sequence and position (one
+ *                         small launch per step) for rbt_hip_routing_history.
  *   "prefill_min_tokens"  smallest T (1..65536, default 12) that takes the grouped path for bf16
  *                         weights: (token, slot) pairs dispatched into per-expert lists and the
  *                         expert FFN run as grouped GEMMs on the matrix cores, each expert's weights
@@ -151,6 +158,34 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
  * discarded). ms_out (may be NULL) receives [prompt ms, generation ms] from HIP events. */
 int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
                      int *n_out, double *ms_out);
+
+/* The same loop printing as the engine does (rabbit2.c:726-729: printf("%d\n") and fflush per token):
+ * on_token(user, id) is called on the calling thread for each generated id in order, as soon as the
+ * device has produced it, up to and including the eos token. The device runs at most 32 steps ahead of
+ * the last reported id and none are queued after the eos token; if on_token returns 0 no further ids
+ * are reported or queued. out [n_gen] and *n_out as rbt_hip_generate (steps already queued when the
+ * output stopped are run and discarded). Each step also copies its id into a pinned host buffer (a
+ * few us per token over rbt_hip_generate). on_token NULL is rbt_hip_generate. */
+typedef int (*rbt_token_fn)(void *user, int32_t token);
+int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos,
+                            rbt_token_fn on_token, void *user, int32_t *out, int *n_out, double *ms_out);
+
+/* Routing of the forward steps run since the last rbt_hip_state_init / rbt_hip_batch_init (with option
+ * "routing_history" set before it): sequence seq, positions [first_pos, first_pos + n_pos), into out
+ * [n_pos][n_layers][top_k] -- what forward() writes to routing_out (rabbit2.c:527) at each position. A
+ * position holds the last step run at it. */
+int rbt_hip_routing_history(rbt_hip *h, int seq, int first_pos, int n_pos, int32_t *out);
+
+/* Host only (no device needed): the engine's expert cache (rabbit2.c:236-300, --expert-cache-mib) replayed
+ * over a routing stream [n_tokens][n_layers][top_k] in the engine's access order (token, layer, slot;
+ * one get_expert per selection, :531-532): the same slots (budget / expert_stride of them, at most
+ * every expert), the same victim rule (first never-filled slot, else least recently used) and the
+ * counters of the engine's stats line (:745-751) into stats = {hits, misses, evictions, bytes_read,
+ * resident_bytes, capacity_bytes}. The experts themselves stay resident in HBM; this reports what the
+ * engine's cache would have done for the same routing. A budget below one expert fails with the
+ * engine's message (:238-242). */
+int rbt_hip_expert_cache_replay(uint64_t budget_bytes, uint64_t expert_stride, int n_layers, int n_experts, int top_k,
+                                const int32_t *routing, uint64_t n_tokens, uint64_t stats[6]);
 
 /* ---- batched decode (no counterpart in the reference, whose State holds one sequence): n_seq
  * independent sequences stepped together, each with its own KV cache of ctx positions. Every weight is

@@ -24,6 +24,8 @@ constexpr uint64_t kAlign = 4096;  // rabbit2.c:56
 constexpr uint64_t kTAlign = 64;   // rabbit2.c:57
 constexpr uint64_t kHeader = 68;   // rabbit2.c:58
 constexpr int kMaxTopK = 64;       // rabbit2.c:59
+// Largest device image rbt_hip_model_create lays out (no file bounds it); hipMalloc decides below it.
+constexpr uint64_t kMaxImageBytes = 1ull << 50;
 
 char g_init_err[512];
 
@@ -108,15 +110,65 @@ struct rbt_hip {
     uint64_t seed = 0;
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
     const int32_t *expert_counts = nullptr;  // histogram of the last grouped-path call
-    // staging for the host-pointer entry points
+    // staging for the host-pointer entry points: device buffer and its pinned host twin
     void *stage = nullptr;
     uint64_t stage_bytes = 0;
+    void *pin = nullptr;
+    uint64_t pin_bytes = 0;
+    // option "routing_history": every forward step also records its routing per sequence and position
+    // (rbt_hip_routing_history), allocated with the decode state
+    int routing_history = 0;
+    int32_t *rhist = nullptr;  // [n_seq][ctx][n_layers][top_k]
+    // pinned host ring the streaming generate reads tokens from
+    int32_t *tok_host = nullptr;
+    int tok_host_n = 0;
     // expert residency counters in the engine's cache-stats terms (rabbit2.c:745-751): every expert is
     // read from the file once at upload (a miss) and every later use of a selected expert is a hit
     uint64_t cache_hits = 0, cache_misses = 0;
 };
 
 namespace {
+
+// Host-side fault injection for the failure-path tests: RBT_HIP_FAULT="<kind>:<n>" makes the n-th
+// (1-based; ":<n>" may be left out for the first) HIP call of that kind in this process report an
+// error without making the call. Kinds: malloc (hipMalloc, hipHostMalloc), launch (kernel launches),
+// copy (hipMemcpy*), sync (stream and event waits). Unset, nothing is injected. The device never sees
+// an injected fault: the call that would have failed is simply not made.
+struct FaultPlan {
+    int kind = -1;  // 0 malloc, 1 launch, 2 copy, 3 sync; -1 none
+    long nth = 1;
+    long seen = 0;
+    FaultPlan() {
+        const char *v = getenv("RBT_HIP_FAULT");
+        if (!v || !*v) return;
+        static const char *const kinds[4] = {"malloc", "launch", "copy", "sync"};
+        for (int k = 0; k < 4; k++) {
+            const size_t n = strlen(kinds[k]);
+            if (strncmp(v, kinds[k], n) == 0 && (v[n] == 0 || v[n] == ':')) {
+                kind = k;
+                if (v[n] == ':') nth = strtol(v + n + 1, nullptr, 10);
+            }
+        }
+    }
+};
+
+int fault_kind(const char *call) {
+    if (strstr(call, "hipMalloc") || strstr(call, "hipHostMalloc")) return 0;
+    if (strncmp(call, "launch_", 7) == 0) return 1;
+    if (strstr(call, "hipMemcpy")) return 2;
+    if (strstr(call, "Synchronize")) return 3;
+    return -1;
+}
+
+hipError_t fault_point(const char *call) {
+    static FaultPlan plan;  // read once per process
+    if (plan.kind < 0 || fault_kind(call) != plan.kind) return hipSuccess;
+    if (++plan.seen != plan.nth) return hipSuccess;
+    static const hipError_t err[4] = {hipErrorOutOfMemory, hipErrorLaunchFailure, hipErrorInvalidValue,
+                                      hipErrorLaunchFailure};
+    fprintf(stderr, "rbt2_hip: RBT_HIP_FAULT: injecting a failure into %.60s\n", call);
+    return err[plan.kind];
+}
 
 int fail(rbt_hip *h, const char *fmt, ...) {
     char buf[512];
@@ -134,9 +186,17 @@ int fail(rbt_hip *h, const char *fmt, ...) {
 
 #define HIP_OK(h, call)                                                                         \
     do {                                                                                        \
-        hipError_t e_ = (call);                                                                 \
+        hipError_t e_ = fault_point(#call);                                                     \
+        if (e_ == hipSuccess) e_ = (call);                                                      \
         if (e_ != hipSuccess) return fail((h), "%s failed: %s", #call, hipGetErrorString(e_)); \
     } while (0)
+
+// A HIP call whose error the caller handles itself, with the same fault injection point.
+#define HIP_TRY(call)                                    \
+    ([&]() -> hipError_t {                               \
+        const hipError_t f_ = fault_point(#call);        \
+        return f_ != hipSuccess ? f_ : (call);           \
+    }())
 
 int set_device(rbt_hip *h) {
     HIP_OK(h, hipSetDevice(h->device));
@@ -145,42 +205,89 @@ int set_device(rbt_hip *h) {
 
 uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
-uint64_t take(uint64_t *off, uint64_t n) {
-    *off = align_up(*off, kTAlign);
-    const uint64_t at = *off;
+// The layout arithmetic runs in 128 bits: header fields are int32, so products such as vocab * dim *
+// 4 can pass 2^64, and an offset that would wrap must still compare as "past the end of the file".
+typedef unsigned __int128 u128;
+u128 align_up128(u128 x, u128 a) { return (x + a - 1) / a * a; }
+u128 take128(u128 *off, u128 n) {
+    *off = align_up128(*off, kTAlign);
+    const u128 at = *off;
     *off += n;
     return at;
 }
+uint64_t sat64(u128 v) { return v > (u128)UINT64_MAX ? UINT64_MAX : (uint64_t)v; }
 
-// rabbit2.c:158-193
-void compute_layout(rbt_hip *h) {
-    const rbt_config &c = h->cfg;
-    const uint64_t E = c.dtype == RBT_DT_BF16 ? 2 : 4, F = 4, D = (uint64_t)c.dim;
-    const uint64_t qd = (uint64_t)c.n_heads * c.head_dim, kvd = (uint64_t)c.n_kv_heads * c.head_dim;
-    uint64_t off = kAlign;
-    h->tok_emb = take(&off, (uint64_t)c.vocab * D * E);
-    h->expert_stride = align_up(3 * (uint64_t)c.expert_hidden * D * E, kAlign);
-    h->layers.assign((size_t)c.n_layers, LayerOff{});
-    for (int l = 0; l < c.n_layers; l++) {
-        LayerOff &ly = h->layers[(size_t)l];
-        ly.attn_norm = take(&off, D * F);
-        ly.wq = take(&off, qd * D * E);
-        ly.wk = take(&off, kvd * D * E);
-        ly.wv = take(&off, kvd * D * E);
-        ly.wo = take(&off, D * qd * E);
-        if (c.qk_norm) {
-            ly.q_norm = take(&off, qd * F);
-            ly.k_norm = take(&off, kvd * F);
-        }
-        ly.ffn_norm = take(&off, D * F);
-        ly.router = take(&off, (uint64_t)c.n_experts * D * E);
-        off = align_up(off, kAlign);
-        ly.experts = off;
-        off += (uint64_t)c.n_experts * h->expert_stride;
+// The offsets of one layer that starts at `off` (rabbit2.c:175-190); returns the offset past its
+// experts (4 KiB aligned).
+u128 layer_offsets(const rbt_config &c, u128 off, u128 stride, LayerOff *ly) {
+    const u128 E = c.dtype == RBT_DT_BF16 ? 2 : 4, F = 4, D = (u128)c.dim;
+    const u128 qd = (u128)c.n_heads * c.head_dim, kvd = (u128)c.n_kv_heads * c.head_dim;
+    LayerOff o{};
+    o.attn_norm = (uint64_t)take128(&off, D * F);
+    o.wq = (uint64_t)take128(&off, qd * D * E);
+    o.wk = (uint64_t)take128(&off, kvd * D * E);
+    o.wv = (uint64_t)take128(&off, kvd * D * E);
+    o.wo = (uint64_t)take128(&off, D * qd * E);
+    if (c.qk_norm) {
+        o.q_norm = (uint64_t)take128(&off, qd * F);
+        o.k_norm = (uint64_t)take128(&off, kvd * F);
     }
-    h->final_norm = take(&off, D * F);
-    h->lm_head = take(&off, (uint64_t)c.vocab * D * E);
-    h->layout_end = h->lm_head + (uint64_t)c.vocab * D * E;
+    o.ffn_norm = (uint64_t)take128(&off, D * F);
+    o.router = (uint64_t)take128(&off, (u128)c.n_experts * D * E);
+    off = align_up128(off, kAlign);
+    o.experts = (uint64_t)off;
+    off += (u128)c.n_experts * stride;
+    if (ly) *ly = o;
+    return off;
+}
+
+// The file layout of a config (rabbit2.c:158-193), computed apart from any handle so that a rejected
+// header leaves the handle's model untouched.
+struct ModelLayout {
+    rbt_config cfg{};
+    uint64_t expert_stride = 0, tok_emb = 0, final_norm = 0, lm_head = 0, layout_end = 0;
+    std::vector<LayerOff> layers;
+};
+
+// Fills *m for config c when its image ends at or before `limit` bytes; returns 0 (with *end_out =
+// the image end, saturated to 2^64 - 1) otherwise, before allocating anything per layer. Layers after
+// the first start 4 KiB aligned (the previous experts end so), so all of them have the first aligned
+// layer's size and the end has a closed form; every layer holds at least one 4 KiB expert stride, so
+// a layout that fits has at most limit / 4096 layers.
+int layout_of(const rbt_config &c, uint64_t limit, ModelLayout *m, uint64_t *end_out) {
+    const u128 E = c.dtype == RBT_DT_BF16 ? 2 : 4, F = 4, D = (u128)c.dim;
+    const u128 stride = align_up128(3 * (u128)c.expert_hidden * D * E, kAlign);
+    u128 off = kAlign;
+    const u128 tok_emb = take128(&off, (u128)c.vocab * D * E);
+    const u128 after0 = layer_offsets(c, off, stride, nullptr);
+    const u128 per_layer = layer_offsets(c, after0, stride, nullptr) - after0;
+    u128 end_layers = after0 + (u128)(c.n_layers - 1) * per_layer;
+    const u128 final_norm = take128(&end_layers, D * F);
+    const u128 lm_head = take128(&end_layers, (u128)c.vocab * D * E);
+    const u128 end = lm_head + (u128)c.vocab * D * E;
+    if (end_out) *end_out = sat64(end);
+    if (end > (u128)limit) return 0;
+    m->cfg = c;
+    m->expert_stride = (uint64_t)stride;
+    m->tok_emb = (uint64_t)tok_emb;
+    m->final_norm = (uint64_t)final_norm;
+    m->lm_head = (uint64_t)lm_head;
+    m->layout_end = (uint64_t)end;
+    m->layers.assign((size_t)c.n_layers, LayerOff{});
+    u128 at = off;
+    for (int l = 0; l < c.n_layers; l++) at = layer_offsets(c, at, stride, &m->layers[(size_t)l]);
+    return 1;
+}
+
+// Makes a validated layout the handle's own (the device image must already hold it).
+void adopt_layout(rbt_hip *h, ModelLayout &&m) {
+    h->cfg = m.cfg;
+    h->expert_stride = m.expert_stride;
+    h->tok_emb = m.tok_emb;
+    h->final_norm = m.final_norm;
+    h->lm_head = m.lm_head;
+    h->layout_end = m.layout_end;
+    h->layers = std::move(m.layers);
 }
 
 int check_layer(rbt_hip *h, const rbt_moe_layer *L) {
@@ -252,6 +359,18 @@ int stage_reserve(rbt_hip *h, uint64_t bytes) {
     return 1;
 }
 
+// The pinned host twin of the stage (copies from and to it run asynchronously at full rate).
+int pin_reserve(rbt_hip *h, uint64_t bytes) {
+    if (bytes <= h->pin_bytes) return 1;
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    if (h->pin) (void)hipHostFree(h->pin);
+    h->pin = nullptr;
+    h->pin_bytes = 0;
+    HIP_OK(h, hipHostMalloc(&h->pin, bytes, hipHostMallocDefault));
+    h->pin_bytes = bytes;
+    return 1;
+}
+
 // The launch context of kernel k: the handle stream, plus (when profiling) the event pair that
 // hipExtLaunchKernel stamps with that kernel's own start and end.
 Launch lc(rbt_hip *h, int k) {
@@ -301,8 +420,8 @@ bool config_ok(const rbt_config &c) {
 
 // The header checks of load_model (rabbit2.c:199-228) on the first bytes of a file of file_size
 // bytes: magic, version 2, a valid config, and a file at least as long as its own layout. On success
-// h->cfg and the layout fields hold the file's (h may be a host-only handle).
-int parse_header(rbt_hip *h, const unsigned char *d, uint64_t file_size, rbt_hip *err_h) {
+// *m holds the file's layout; nothing else is touched (errors go to err_h, which may be NULL).
+int parse_header(ModelLayout *m, const unsigned char *d, uint64_t file_size, rbt_hip *err_h) {
     if (!d || file_size < kHeader || memcmp(d, "RBT2", 4) != 0) return fail(err_h, "bad magic: not a .rbt2 file");
     uint32_t version;
     memcpy(&version, d + 4, 4);
@@ -310,27 +429,39 @@ int parse_header(rbt_hip *h, const unsigned char *d, uint64_t file_size, rbt_hip
     rbt_config c;
     memcpy(&c, d + 8, sizeof c);
     if (!config_ok(c)) return fail(err_h, "invalid config in header");
-    h->cfg = c;
-    compute_layout(h);
-    if (h->layout_end > file_size)
+    uint64_t end = 0;
+    if (!layout_of(c, file_size, m, &end))
         return fail(err_h, "file too small for its own config (%llu < %llu)", (unsigned long long)file_size,
-                    (unsigned long long)h->layout_end);
+                    (unsigned long long)end);
     return 1;
 }
 
-// (Re)allocates the device image for h->cfg's layout; drops any decode state of an earlier model.
-int model_alloc(rbt_hip *h) {
+// Drops the handle's model image and decode state (the workspace stays: it depends on shapes only).
+// Afterwards the handle holds no model until a new layout is adopted with its image.
+int model_drop(rbt_hip *h) {
     if (!set_device(h)) return 0;
     HIP_OK(h, hipStreamSynchronize(h->stream));
     (void)hipFree(h->ds.block);
     h->ds = DecodeState{};
-    if (h->model) {
-        (void)hipFree(h->model);
-        h->model = nullptr;
-        h->model_size = 0;
-    }
-    HIP_OK(h, hipMalloc(&h->model, h->layout_end));
-    h->model_size = h->layout_end;
+    (void)hipFree(h->rhist);
+    h->rhist = nullptr;
+    if (h->model) (void)hipFree(h->model);
+    h->model = nullptr;
+    h->model_size = 0;
+    h->cfg = rbt_config{};
+    h->layers.clear();
+    h->expert_stride = h->tok_emb = h->final_norm = h->lm_head = h->layout_end = 0;
+    return 1;
+}
+
+// Replaces the handle's model with a fresh device image of layout m (contents left to the caller).
+// On failure the handle holds no model.
+int model_alloc(rbt_hip *h, const ModelLayout &m) {
+    if (!model_drop(h)) return 0;
+    void *p = nullptr;
+    HIP_OK(h, hipMalloc(&p, m.layout_end));
+    h->model = static_cast<uint8_t *>(p);
+    h->model_size = m.layout_end;
     return 1;
 }
 
@@ -354,9 +485,14 @@ int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float 
     HIP_OK(h, launch_topk_split(lc(h, kProfTopk), w.probs, T, L->n_experts, L->top_k, L->norm_topk, xb, L->dim, routing,
                                 w.weights, x_hi, x_lo));
     int32_t *counts = nullptr;
-    HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
-                             L->experts, L->expert_stride, xb, T, L->n_experts, L->top_k, L->dim, L->expert_hidden,
-                             routing, w.weights, w.hbuf, w.pre, x, nullptr, &counts, true, next_nw == nullptr));
+    // the combine's event pair is taken only by the launch that runs it (launch_prefill's combine, or
+    // the fused combine + RMSNorm below), so a deferred-profile pair is never left unrecorded
+    Launch no_combine;
+    no_combine.s = h->stream;
+    HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown),
+                             next_nw ? no_combine : lc(h, kProfCombine), L->experts, L->expert_stride, xb, T,
+                             L->n_experts, L->top_k, L->dim, L->expert_hidden, routing, w.weights, w.hbuf, w.pre, x,
+                             nullptr, &counts, true, next_nw == nullptr));
     h->expert_counts = counts;
     if (next_nw) {  // the combine, fused with the RMSNorm the next step starts with (xb and its planes)
         const float *y = nullptr;
@@ -492,6 +628,8 @@ int enqueue_step(rbt_hip *h, bool final) {
             if (!rbt_hip_moe_dev(h, &ml, ds.xb, B, ds.x, nullptr, routing, nullptr)) return 0;
         }
     }
+    if (h->rhist)  // the step's routing into each sequence's history, at the position not yet advanced
+        STEP_LAUNCH(-1, launch_record_routing(L, ds.st, ds.routing, c.n_layers, c.top_k, B, ds.ctx, h->rhist));
     if (final) {
         const void *W[3] = {h->model + h->lm_head, nullptr, nullptr};
         float *const out[3] = {ds.logits, nullptr, nullptr};
@@ -585,6 +723,9 @@ void rbt_hip_free(rbt_hip *h) {
         for (hipEvent_t ev : h->prof.pool[k]) (void)hipEventDestroy(ev);
     }
     (void)hipFree(h->stage);
+    if (h->pin) (void)hipHostFree(h->pin);
+    (void)hipFree(h->rhist);
+    if (h->tok_host) (void)hipHostFree(h->tok_host);
     (void)hipFree(h->model);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
@@ -601,10 +742,16 @@ int rbt_hip_set_router_order(rbt_hip *h, int order) {
 
 int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config *cfg) {
     if (!h) return fail(nullptr, "upload: handle is NULL");
-    if (!parse_header(h, static_cast<const unsigned char *>(file), file_size, h)) return 0;
-    const rbt_config c = h->cfg;
-    if (!model_alloc(h)) return 0;
-    HIP_OK(h, hipMemcpy(h->model, file, h->layout_end, hipMemcpyHostToDevice));
+    ModelLayout m;
+    if (!parse_header(&m, static_cast<const unsigned char *>(file), file_size, h)) return 0;
+    if (!model_alloc(h, m)) return 0;
+    const hipError_t e = HIP_TRY(hipMemcpy(h->model, file, m.layout_end, hipMemcpyHostToDevice));
+    if (e != hipSuccess) {
+        model_drop(h);
+        return fail(h, "upload: hipMemcpy failed: %s", hipGetErrorString(e));
+    }
+    const rbt_config c = m.cfg;
+    adopt_layout(h, std::move(m));
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
@@ -626,28 +773,27 @@ int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
     unsigned char hdr[kHeader];
     if (file_size < kHeader || pread(fd, hdr, kHeader, 0) != (ssize_t)kHeader)
         return fail(h, "bad magic: not a .rbt2 file");
-    if (!parse_header(h, hdr, file_size, h)) return 0;
-    const rbt_config c = h->cfg;
-    if (!model_alloc(h)) return 0;
+    ModelLayout m;
+    if (!parse_header(&m, hdr, file_size, h)) return 0;
     // the file mapped read-only (rabbit2.c:141-147) and copied in one call: the runtime pipelines a
     // pageable source through its own pinned staging (measured ~29 GB/s from the page cache, three
     // times a pread loop over pinned buffers)
-    void *map = mmap(nullptr, (size_t)h->layout_end, PROT_READ, MAP_SHARED, fd, 0);
-    if (map == MAP_FAILED) {
-        (void)hipFree(h->model);
-        h->model = nullptr;
-        h->model_size = 0;
-        return fail(h, "cannot map %s", path);
-    }
-    (void)madvise(map, (size_t)h->layout_end, MADV_SEQUENTIAL);
-    const hipError_t e = hipMemcpy(h->model, map, h->layout_end, hipMemcpyHostToDevice);
-    munmap(map, (size_t)h->layout_end);
+    void *map = mmap(nullptr, (size_t)m.layout_end, PROT_READ, MAP_SHARED, fd, 0);
+    if (map == MAP_FAILED) return fail(h, "cannot map %s", path);
+    struct Unmap {
+        void *p;
+        size_t n;
+        ~Unmap() { munmap(p, n); }
+    } unmap{map, (size_t)m.layout_end};
+    if (!model_alloc(h, m)) return 0;
+    (void)madvise(map, (size_t)m.layout_end, MADV_SEQUENTIAL);
+    const hipError_t e = HIP_TRY(hipMemcpy(h->model, map, m.layout_end, hipMemcpyHostToDevice));
     if (e != hipSuccess) {
-        (void)hipFree(h->model);
-        h->model = nullptr;
-        h->model_size = 0;
+        model_drop(h);
         return fail(h, "upload_file: hipMemcpy failed: %s", hipGetErrorString(e));
     }
+    const rbt_config c = m.cfg;
+    adopt_layout(h, std::move(m));
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
@@ -668,7 +814,7 @@ int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]) {
     unsigned char hdr[kHeader];
     if (file_size < kHeader || pread(fd, hdr, kHeader, 0) != (ssize_t)kHeader)
         return fail(nullptr, "bad magic: not a .rbt2 file");
-    rbt_hip tmp;  // host-only: no device, no stream
+    ModelLayout tmp;  // host-only: no device, no stream
     if (!parse_header(&tmp, hdr, file_size, nullptr)) return 0;
     if (cfg) *cfg = tmp.cfg;
     if (info) {
@@ -701,9 +847,15 @@ int rbt_hip_model_create(rbt_hip *h, const rbt_config *cfg, void **model_dev) {
     if (!cfg || !model_dev) return fail(h, "model_create: NULL argument");
     *model_dev = nullptr;
     if (!config_ok(*cfg)) return fail(h, "model_create: invalid config");
-    h->cfg = *cfg;
-    compute_layout(h);
-    if (!model_alloc(h)) return 0;
+    ModelLayout m;
+    uint64_t end = 0;
+    if (!layout_of(*cfg, kMaxImageBytes, &m, &end))
+        return fail(h, "model_create: the image of this config (%llu bytes) exceeds %llu bytes",
+                    (unsigned long long)end, (unsigned long long)kMaxImageBytes);
+    if (!model_alloc(h, m)) return 0;
+    adopt_layout(h, std::move(m));
+    h->cache_hits = 0;
+    h->cache_misses = (uint64_t)cfg->n_layers * cfg->n_experts;
     *model_dev = h->model;
     return 1;
 }
@@ -850,19 +1002,23 @@ int rbt_hip_moe(rbt_hip *h, int layer, const float *xb, int T, float *x_inout, i
     if (T < 0) return fail(h, "moe: negative token count");
     if (T == 0) return 1;
     if (!xb) return fail(h, "moe: xb is NULL");
+    // one region [xb | x | routing] on the device and its pinned host twin: the inputs go up in one copy,
+    // x and the routing come back in one, and the call waits once
     const uint64_t nx = (uint64_t)T * L.dim, nr = (uint64_t)T * L.top_k;
-    const uint64_t xb_off = 0, x_off = align_up(nx * 4, 256), r_off = x_off + align_up(nx * 4, 256);
-    if (!set_device(h) || !stage_reserve(h, r_off + nr * 4)) return 0;
-    uint8_t *st = static_cast<uint8_t *>(h->stage);
-    float *xb_d = reinterpret_cast<float *>(st + xb_off);
+    const uint64_t x_off = align_up(nx * 4, 256), r_off = x_off + align_up(nx * 4, 256), total = r_off + nr * 4;
+    if (!set_device(h) || !stage_reserve(h, total) || !pin_reserve(h, total)) return 0;
+    uint8_t *st = static_cast<uint8_t *>(h->stage), *pn = static_cast<uint8_t *>(h->pin);
     float *x_d = x_inout ? reinterpret_cast<float *>(st + x_off) : nullptr;
     int32_t *r_d = reinterpret_cast<int32_t *>(st + r_off);
-    HIP_OK(h, hipMemcpyAsync(xb_d, xb, nx * 4, hipMemcpyHostToDevice, h->stream));
-    if (x_d) HIP_OK(h, hipMemcpyAsync(x_d, x_inout, nx * 4, hipMemcpyHostToDevice, h->stream));
-    if (!rbt_hip_moe_dev(h, &L, xb_d, T, x_d, nullptr, r_d, nullptr)) return 0;
-    if (x_d) HIP_OK(h, hipMemcpyAsync(x_inout, x_d, nx * 4, hipMemcpyDeviceToHost, h->stream));
-    if (routing_out) HIP_OK(h, hipMemcpyAsync(routing_out, r_d, nr * 4, hipMemcpyDeviceToHost, h->stream));
+    memcpy(pn, xb, nx * 4);
+    if (x_inout) memcpy(pn + x_off, x_inout, nx * 4);
+    HIP_OK(h, hipMemcpyAsync(st, pn, x_inout ? x_off + nx * 4 : nx * 4, hipMemcpyHostToDevice, h->stream));
+    if (!rbt_hip_moe_dev(h, &L, reinterpret_cast<float *>(st), T, x_d, nullptr, r_d, nullptr)) return 0;
+    const uint64_t back = x_inout ? x_off : r_off;  // x (if any) and the routing, one contiguous copy
+    HIP_OK(h, hipMemcpyAsync(pn + back, st + back, total - back, hipMemcpyDeviceToHost, h->stream));
     HIP_OK(h, hipStreamSynchronize(h->stream));
+    if (x_inout) memcpy(x_inout, pn + x_off, nx * 4);
+    if (routing_out) memcpy(routing_out, pn + r_off, nr * 4);
     h->cache_hits += nr;  // every selected expert was resident
     return 1;
 }
@@ -969,6 +1125,8 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
         h->fused_decode = value != 0;
     } else if (strcmp(name, "batch_mfma") == 0) {
         h->batch_mfma = value != 0;
+    } else if (strcmp(name, "routing_history") == 0) {
+        h->routing_history = value != 0;  // takes effect at the next rbt_hip_state_init / batch_init
     } else if (strcmp(name, "prefill_min_tokens") == 0) {
         if (value < 1 || value > 65536) return fail(h, "set_option: prefill_min_tokens must be in [1, 65536]");
         h->prefill_min_tokens = (int)value;
@@ -1049,6 +1207,8 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     HIP_OK(h, hipStreamSynchronize(h->stream));
     (void)hipFree(h->ds.block);
     h->ds = DecodeState{};
+    (void)hipFree(h->rhist);
+    h->rhist = nullptr;
     DecodeState ds;
     ds.n_seq = n_seq;
     ds.ctx = ctx;
@@ -1118,6 +1278,17 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
             return fail(h, "state_init: hipMemcpy failed: %s", hipGetErrorString(e));
         }
     }
+    if (h->routing_history) {
+        const size_t hb = sizeof(int32_t) * (size_t)n_seq * ctx * c.n_layers * c.top_k;
+        hipError_t e = HIP_TRY(hipMalloc(&h->rhist, hb));
+        if (e == hipSuccess) e = HIP_TRY(hipMemset(h->rhist, 0, hb));
+        if (e != hipSuccess) {
+            (void)hipFree(h->rhist);
+            (void)hipFree(ds.block);
+            h->rhist = nullptr;
+            return fail(h, "state_init: hipMalloc of the routing history failed: %s", hipGetErrorString(e));
+        }
+    }
     h->ds = ds;
     // the MoE workspace for n_seq tokens per layer call, so that no step allocates
     rbt_moe_layer ml;
@@ -1152,6 +1323,11 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
 
 int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
                      int *n_out, double *ms_out) {
+    return rbt_hip_generate_stream(h, prompt, n_prompt, n_gen, eos, nullptr, nullptr, out, n_out, ms_out);
+}
+
+int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos,
+                            rbt_token_fn on_token, void *user, int32_t *out, int *n_out, double *ms_out) {
     if (!h) return fail(nullptr, "generate: handle is NULL");
     if (n_out) *n_out = 0;
     if (!h->ds.block) return fail(h, "generate: no decode state (rbt_hip_state_init)");
@@ -1167,6 +1343,14 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
     if (n_gen > ctx - n_prompt) n_gen = ctx - n_prompt;  // rabbit2.c:717
     if (n_gen > 0 && !out) return fail(h, "generate: out is NULL");
     if (!set_device(h)) return 0;
+    if (on_token && n_gen > h->tok_host_n) {  // the pinned ring the device's tokens are copied into
+        HIP_OK(h, hipStreamSynchronize(h->stream));
+        if (h->tok_host) (void)hipHostFree(h->tok_host);
+        h->tok_host = nullptr;
+        h->tok_host_n = 0;
+        HIP_OK(h, hipHostMalloc(&h->tok_host, sizeof(int32_t) * (size_t)n_gen, hipHostMallocDefault));
+        h->tok_host_n = n_gen;
+    }
     const StepState st{0, n_prompt, 0, 0, h->seed ? h->seed : 0x9E3779B97F4A7C15ull, 0};  // rabbit2.c:723
     HIP_OK(h, hipMemcpyAsync(h->ds.seq, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, h->stream));
     HIP_OK(h, hipMemcpyAsync(h->ds.st, &st, sizeof st, hipMemcpyHostToDevice, h->stream));
@@ -1174,6 +1358,10 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
     h->prof.mode = 0;
     hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    // streaming: one event per step in flight; the host keeps at most kStreamAhead steps queued past
+    // the last token it has reported, and stops queueing at the eos token
+    constexpr int kStreamAhead = 32;
+    hipEvent_t ring[kStreamAhead] = {};
     int ok = capture_step(h, false, &g_adv) && capture_step(h, true, &g_fin);
     h->prof.mode = prof;
     auto cleanup = [&]() {
@@ -1181,24 +1369,73 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
         if (g_fin) (void)hipGraphExecDestroy(g_fin);
         for (hipEvent_t e : ev)
             if (e) (void)hipEventDestroy(e);
+        for (hipEvent_t e : ring)
+            if (e) (void)hipEventDestroy(e);
     };
     if (!ok) {
         cleanup();
         return 0;
     }
     hipError_t e = hipSuccess;
-    for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);
+    for (int i = 0; i < 3 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
     if (e == hipSuccess) e = hipEventRecord(ev[0], h->stream);
     // the prompt: n_prompt forwards, the last one with lm_head + argmax (the first generated token)
-    for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = hipGraphLaunch(g_adv, h->stream);
-    if (e == hipSuccess && n_gen > 0) e = hipGraphLaunch(g_fin, h->stream);
-    if (e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
-    // each further token: one forward of the previous one (rabbit2.c:733)
-    for (int g = 1; g < n_gen && e == hipSuccess; g++) e = hipGraphLaunch(g_fin, h->stream);
-    if (e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
-    if (e == hipSuccess && n_gen > 0)
-        e = hipMemcpyAsync(out, h->ds.seq + n_prompt, 4 * (size_t)n_gen, hipMemcpyDeviceToHost, h->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+    for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = HIP_TRY(hipGraphLaunch(g_adv, h->stream));
+    int n = n_gen;
+    if (!on_token) {
+        if (e == hipSuccess && n_gen > 0) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        if (e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
+        // each further token: one forward of the previous one (rabbit2.c:733)
+        for (int g = 1; g < n_gen && e == hipSuccess; g++) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        if (e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+        if (e == hipSuccess && n_gen > 0)
+            e = HIP_TRY(hipMemcpyAsync(out, h->ds.seq + n_prompt, 4 * (size_t)n_gen, hipMemcpyDeviceToHost, h->stream));
+        if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
+        for (int g = 0; g < n_gen && e == hipSuccess; g++)
+            if (out[g] == eos) {  // the engine prints the eos token, then stops (rabbit2.c:729-730)
+                n = g + 1;
+                break;
+            }
+    } else {
+        for (int i = 0; i < kStreamAhead && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ring[i]));
+        int queued = 0, reported = 0;
+        bool more = n_gen > 0, report = true;
+        auto queue_step = [&](int g) -> hipError_t {
+            hipError_t r = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+            if (r == hipSuccess && g == 0) r = hipEventRecord(ev[1], h->stream);
+            if (r == hipSuccess)
+                r = HIP_TRY(hipMemcpyAsync(h->tok_host + g, h->ds.seq + n_prompt + g, 4, hipMemcpyDeviceToHost,
+                                           h->stream));
+            if (r == hipSuccess) r = hipEventRecord(ring[g % kStreamAhead], h->stream);
+            return r;
+        };
+        n = 0;
+        while (e == hipSuccess && reported < queued + (more ? 1 : 0)) {
+            while (e == hipSuccess && more && queued < reported + kStreamAhead) {
+                e = queue_step(queued++);
+                if (queued == n_gen) more = false;
+                if (!more && e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+            }
+            if (e != hipSuccess || reported == queued) break;
+            e = HIP_TRY(hipEventSynchronize(ring[reported % kStreamAhead]));
+            if (e != hipSuccess) break;
+            const int32_t tok = h->tok_host[reported];
+            out[reported++] = tok;
+            n = reported;
+            if (report && !on_token(user, tok)) report = false;  // the caller wants no more tokens
+            if (tok == eos || !report) {  // nothing more is queued; the queued steps run to their end
+                if (more) {
+                    more = false;
+                    e = hipEventRecord(ev[2], h->stream);
+                }
+                break;
+            }
+        }
+        if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
+        if (n_gen == 0 && e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
+        if (n_gen == 0 && e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+        if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
+    }
     if (e == hipSuccess && ms_out) {
         float a = 0.0f, b = 0.0f;
         e = hipEventElapsedTime(&a, ev[0], ev[1]);
@@ -1208,12 +1445,6 @@ int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen,
     }
     cleanup();
     if (e != hipSuccess) return fail(h, "generate: %s", hipGetErrorString(e));
-    int n = n_gen;
-    for (int g = 0; g < n_gen; g++)
-        if (out[g] == eos) {  // the engine prints the eos token, then stops (rabbit2.c:729-730)
-            n = g + 1;
-            break;
-        }
     if (n_out) *n_out = n;
     return 1;
 }
@@ -1302,6 +1533,86 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
         if (ei) (void)hipEventDestroy(ei);
     if (!ok) return 0;
     if (e != hipSuccess) return fail(h, "generate_batch: %s", hipGetErrorString(e));
+    return 1;
+}
+
+int rbt_hip_routing_history(rbt_hip *h, int seq, int first_pos, int n_pos, int32_t *out) {
+    if (!h) return fail(nullptr, "routing_history: handle is NULL");
+    if (!h->ds.block) return fail(h, "routing_history: no decode state");
+    if (!h->rhist) return fail(h, "routing_history: option \"routing_history\" was off at rbt_hip_state_init");
+    if (seq < 0 || seq >= h->ds.n_seq) return fail(h, "routing_history: sequence %d out of range", seq);
+    if (first_pos < 0 || n_pos < 0 || first_pos > h->ds.ctx - n_pos)
+        return fail(h, "routing_history: positions [%d, %d) outside the context of %d", first_pos, first_pos + n_pos,
+                    h->ds.ctx);
+    if (n_pos == 0) return 1;
+    if (!out) return fail(h, "routing_history: out is NULL");
+    if (!set_device(h)) return 0;
+    const size_t per = (size_t)h->cfg.n_layers * h->cfg.top_k;
+    HIP_OK(h, hipMemcpyAsync(out, h->rhist + ((size_t)seq * h->ds.ctx + first_pos) * per, 4 * per * (size_t)n_pos,
+                             hipMemcpyDeviceToHost, h->stream));
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    return 1;
+}
+
+int rbt_hip_expert_cache_replay(uint64_t budget_bytes, uint64_t expert_stride, int n_layers, int n_experts, int top_k,
+                                const int32_t *routing, uint64_t n_tokens, uint64_t stats[6]) {
+    if (!stats || (n_tokens && !routing)) return fail(nullptr, "expert_cache_replay: NULL argument");
+    if (expert_stride == 0 || n_layers <= 0 || n_experts <= 0 || top_k <= 0)
+        return fail(nullptr, "expert_cache_replay: invalid shape");
+    if (budget_bytes < expert_stride)  // rabbit2.c:238-242
+        return fail(nullptr, "expert cache budget too small: need at least %llu bytes for one expert",
+                    (unsigned long long)expert_stride);
+    // expert_cache_init (rabbit2.c:243-245): as many whole slots as the budget holds, at most every expert
+    uint64_t cap = budget_bytes / expert_stride;
+    const uint64_t total = (uint64_t)n_layers * (uint64_t)n_experts;
+    if (cap > total) cap = total;
+    struct Slot {
+        int layer = -1, expert = -1;
+        uint64_t last_used = 0;
+        bool valid = false, has_data = false;
+    };
+    std::vector<Slot> slots((size_t)cap);
+    uint64_t clock = 0, hits = 0, misses = 0, evictions = 0, resident = 0;
+    // get_expert (rabbit2.c:261-300) for every selection in the engine's order: token, layer, slot
+    for (uint64_t t = 0; t < n_tokens; t++)
+        for (int l = 0; l < n_layers; l++)
+            for (int k = 0; k < top_k; k++) {
+                const int e = routing[(t * (uint64_t)n_layers + (uint64_t)l) * (uint64_t)top_k + (uint64_t)k];
+                if (e < 0 || e >= n_experts)
+                    return fail(nullptr, "expert_cache_replay: expert %d out of range (token %llu, layer %d)", e,
+                                (unsigned long long)t, l);
+                Slot *victim = nullptr;
+                bool hit = false;
+                for (Slot &sl : slots) {
+                    if (sl.valid && sl.layer == l && sl.expert == e) {
+                        sl.last_used = ++clock;
+                        hits++;
+                        hit = true;
+                        break;
+                    }
+                    // the first never-filled slot, else the least recently used one
+                    if (!victim || (!sl.valid && victim->valid) ||
+                        (sl.valid == victim->valid && sl.last_used < victim->last_used))
+                        victim = &sl;
+                }
+                if (hit) continue;
+                misses++;
+                if (!victim->has_data) {
+                    victim->has_data = true;
+                    resident++;
+                }
+                if (victim->valid) evictions++;
+                victim->layer = l;
+                victim->expert = e;
+                victim->last_used = ++clock;
+                victim->valid = true;
+            }
+    stats[0] = hits;
+    stats[1] = misses;
+    stats[2] = evictions;
+    stats[3] = misses * expert_stride;    // bytes_read: one stride per miss
+    stats[4] = resident * expert_stride;  // resident_bytes
+    stats[5] = cap * expert_stride;       // capacity_bytes
     return 1;
 }
 

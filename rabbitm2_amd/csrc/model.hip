@@ -1227,6 +1227,22 @@ __global__ void advance_kernel(StepState *st, int B) {
     if (b < B) st[b].pos = st[b].pos + 1;
 }
 
+// The step's routing [n_layers][B][K] copied into each sequence's history [B][ctx][n_layers][K] at the
+// step's position (before the step advances it). Grid: B blocks of 256 threads.
+__global__ __launch_bounds__(256) void record_routing_kernel(const StepState *__restrict__ st,
+                                                             const int32_t *__restrict__ routing, int n_layers, int K,
+                                                             int B, int ctx, int32_t *__restrict__ hist) {
+    const int b = blockIdx.x;
+    const int pos = st[b].pos;
+    if (pos < 0 || pos >= ctx) return;
+    const int per = n_layers * K;
+    int32_t *dst = hist + ((size_t)b * ctx + pos) * per;
+    for (int i = threadIdx.x; i < per; i += blockDim.x) {
+        const int l = i / K, k = i - l * K;
+        dst[i] = routing[((size_t)l * B + b) * K + k];
+    }
+}
+
 inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // The specialised dense kernel when rows are whole 1 KiB wave-steps (D = 512 * NC bf16 / 256 * NC f32,
@@ -1528,6 +1544,11 @@ hipError_t launch_sample(const Launch &L, const float *logits, int n, const Samp
 
 hipError_t launch_advance(const Launch &L, StepState *st, int B) {
     return launch(L, advance_kernel, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, st, B);
+}
+
+hipError_t launch_record_routing(const Launch &L, const StepState *st, const int32_t *routing, int n_layers, int K,
+                                 int B, int ctx, int32_t *hist) {
+    return launch(L, record_routing_kernel, dim3((unsigned)B), dim3(256), 0, st, routing, n_layers, K, B, ctx, hist);
 }
 
 }  // namespace rbt

@@ -260,6 +260,10 @@ __device__ __forceinline__ size_t mfma_plane_index(int t, int k, int TB) {
 }
 hipError_t launch_argmax(const Launch &L, const float *v, int n, StepState *st, int32_t *seq, int ctx, int B);
 hipError_t launch_advance(const Launch &L, StepState *st, int B);
+// Copies the step's routing [n_layers][B][K] into hist [B][ctx][n_layers][K] at each sequence's
+// current position (run before the step advances).
+hipError_t launch_record_routing(const Launch &L, const StepState *st, const int32_t *routing, int n_layers, int K,
+                                 int B, int ctx, int32_t *hist);
 
 // Dense matvec (one row per wave).
 hipError_t launch_matvec(const Launch &L, int dtype, const void *W, const float *x, float *out, int rows, int cols);

@@ -23,7 +23,10 @@ EXPORTS = (
     "rbt_hip_profile_get", "rbt_hip_set_option", "rbt_hip_state_init", "rbt_hip_forward", "rbt_hip_generate",
     "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
     "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling", "rbt_hip_file_info",
+    "rbt_hip_generate_stream", "rbt_hip_routing_history", "rbt_hip_expert_cache_replay",
 )
+
+TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32)
 
 
 class Config(C.Structure):
@@ -88,6 +91,11 @@ def lib():
         L.rbt_hip_set_sampling.argtypes = [vp, f32, i32, f32, u64]
         L.rbt_hip_forward_batch.argtypes = [vp, vp, vp, vp, vp]
         L.rbt_hip_generate_batch.argtypes = [vp, vp, i32, i32, vp, C.POINTER(C.c_double)]
+        L.rbt_hip_generate_stream.argtypes = [vp, vp, i32, i32, C.c_int32, TOKEN_FN, vp, vp, C.POINTER(C.c_int),
+                                              C.POINTER(C.c_double)]
+        L.rbt_hip_routing_history.argtypes = [vp, i32, i32, i32, vp]
+        L.rbt_hip_expert_cache_replay.argtypes = [u64, u64, i32, i32, i32, vp, u64, C.POINTER(C.c_uint64)]
+        L.rbt_hip_file_info.argtypes = [C.c_char_p, C.POINTER(Config), C.POINTER(C.c_uint64)]
         _lib = L
     return _lib
 
@@ -297,6 +305,29 @@ class Device:
                                             C.byref(n), ms))
         return out[:n.value].tolist(), (ms[0], ms[1])
 
+    def generate_stream(self, prompt, n_gen, eos=-1, stop_after=None):
+        """The streaming --gen loop: (ids reported one by one through the callback, the ids of out,
+        [prompt ms, generation ms]). stop_after: the callback returns 0 after that many ids."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(max(n_gen, 1), np.int32)
+        n = C.c_int(0)
+        ms = (C.c_double * 2)()
+        seen = []
+
+        def on_token(_user, tok):
+            seen.append(int(tok))
+            return 0 if stop_after is not None and len(seen) >= stop_after else 1
+
+        fn = TOKEN_FN(on_token)
+        self._check(self.L.rbt_hip_generate_stream(self.h, _p(prompt), prompt.size, int(n_gen), int(eos), fn, None,
+                                                   _p(out), C.byref(n), ms))
+        return seen, out[:n.value].tolist(), (ms[0], ms[1])
+
+    def routing_history(self, seq, first_pos, n_pos, n_layers, top_k):
+        out = np.zeros((max(n_pos, 1), n_layers, top_k), np.int32)
+        self._check(self.L.rbt_hip_routing_history(self.h, seq, first_pos, n_pos, _p(out)))
+        return out[:n_pos]
+
     # ---- device level
     def moe_dev(self, layer, xb, T, x=None, moe=None, routing=None, weights=None):
         vp = lambda b: None if b is None else (b if isinstance(b, C.c_void_p) else b.p)
@@ -317,6 +348,16 @@ class Device:
     def matvec_dev(self, out, W, dtype, x, rows, cols):
         self._check(self.L.rbt_hip_matvec_dev(self.h, out.p, W if isinstance(W, C.c_void_p) else W.p, dtype, x.p,
                                               rows, cols))
+
+
+def expert_cache_replay(budget_bytes, expert_stride, routing, n_experts):
+    """The engine's expert LRU replayed over routing [T][n_layers][top_k] (host only): the stats dict."""
+    routing = np.ascontiguousarray(routing, dtype=np.int32)
+    T, n_layers, top_k = routing.shape
+    a = (C.c_uint64 * 6)()
+    if not lib().rbt_hip_expert_cache_replay(budget_bytes, expert_stride, n_layers, n_experts, top_k, _p(routing), T, a):
+        raise HipError(lib().rbt_hip_last_error(None).decode())
+    return dict(zip(("hits", "misses", "evictions", "bytes_read", "resident_bytes", "capacity_bytes"), a))
 
 
 def moe_layer_desc(dim, n_experts, top_k, hidden, dtype, norm_topk, router, experts, stride, bias=None):

@@ -8,14 +8,20 @@
  * expert-cache line go to stderr (:742-751). Exit codes: 0 ok, 1 runtime error, 2 usage.
  *
  * Everything past argument parsing runs through the C ABI of include/rbt2_hip.h: the .rbt2 image is
- * copied to HBM once (every expert resident, so --expert-cache-mib only keeps its checks and its
- * stats line), the KV cache lives in HBM, and each forward() is the library's per-token pass on
- * hand-written gfx950 kernels. --gen runs the whole loop on the device (rbt_hip_generate), so the
- * ids are printed when the loop ends rather than one by one.
+ * copied to HBM once, the KV cache lives in HBM, and each forward() is the library's per-token pass on
+ * hand-written gfx950 kernels. --gen runs the loop on the device (rbt_hip_generate_stream) and prints
+ * each id with a flush as soon as the device has produced it, as the engine does (rabbit2.c:726-729).
  *
- * --kernel keeps its meaning as the CPU summation order that expert selection reproduces bit for bit:
- * no flag or "scalar" -> the engine's scalar order (its default, rabbit2.c:312); "avx2" -> the AVX2
- * order; "auto" or "hip" -> AVX2 when this host has it, as the engine's auto would pick.
+ * --kernel keeps its meaning as the CPU summation order that expert selection reproduces bit for bit,
+ * and prints the engine's line for it (rabbit2.c:652-661): no flag or "scalar" -> the engine's scalar
+ * order (its default, rabbit2.c:312), "matvec kernel: scalar"; "avx2" -> the AVX2 order, "matvec
+ * kernel: avx2" (reproduced on the device whatever the host CPU); "auto" -> AVX2 when this host has it,
+ * as the engine's auto picks; "hip" -> the same order as auto, printed as "matvec kernel: hip-gfx950".
+ *
+ * --expert-cache-mib: every expert is resident in HBM, so no expert is read from the file after the
+ * upload; the budget checks are the engine's (rabbit2.c:238-242, :640-648), and the stats line
+ * (:745-751) reports what the engine's LRU cache would have done for the same routing, replayed over
+ * the routing of every forward() the engine would have run (rbt_hip_expert_cache_replay).
  */
 #define _POSIX_C_SOURCE 200809L /* clock_gettime under -std=c99 */
 #include <errno.h>
@@ -51,18 +57,29 @@ static void usage(const char *p) {
             p, p, p);
 }
 
-/* Runs the engine with the model loaded on device 0; returns the process exit code. */
-static int run(const char *path, const rbt_config *c, int order, int ctx, const int32_t *tokens, int nt,
-               const char *dump_l, const char *dump_r, int gen, int eos, float temperature, int top_k_sample,
-               float top_p, unsigned long long seed, int cache_stats) {
+/* The engine's gen-loop output: one id per line, flushed (rabbit2.c:728-729). */
+static int print_token(void *user, int32_t token) {
+    (void)user;
+    printf("%d\n", token);
+    fflush(stdout);
+    return 1;
+}
+
+/* Runs the engine with the model loaded on device 0; returns the process exit code. cache_budget > 0:
+ * print the engine's expert-cache line for that budget. */
+static int run(const char *path, const rbt_config *c, uint64_t expert_stride, int order, int ctx,
+               const int32_t *tokens, int nt, const char *dump_l, const char *dump_r, int gen, int eos,
+               float temperature, int top_k_sample, float top_p, unsigned long long seed,
+               unsigned long long cache_budget) {
     rbt_hip *h = NULL;
     if (!rbt_hip_init(&h, 0)) return 1; /* the library printed the reason */
     int rc = 1;
     float *logits = NULL;
-    int32_t *routing = NULL, *ids = NULL;
+    int32_t *routing = NULL, *ids = NULL, *hist = NULL;
     FILE *fl = NULL, *fr = NULL;
-    if (!rbt_hip_set_router_order(h, order) || !rbt_hip_upload_file(h, path, NULL) || !rbt_hip_state_init(h, ctx))
-        goto done;
+    if (!rbt_hip_set_router_order(h, order) || !rbt_hip_upload_file(h, path, NULL)) goto done;
+    if (cache_budget && !rbt_hip_set_option(h, "routing_history", 1)) goto done;
+    if (!rbt_hip_state_init(h, ctx)) goto done;
 
     logits = (float *)malloc(sizeof(float) * (size_t)c->vocab);
     routing = (int32_t *)calloc((size_t)c->n_layers * c->top_k, sizeof(int32_t));
@@ -100,26 +117,35 @@ static int run(const char *path, const rbt_config *c, int order, int ctx, const 
         }
         if (temperature > 0.0f && !rbt_hip_set_sampling(h, temperature, top_k_sample, top_p, (uint64_t)seed))
             goto done;
-        /* the device loop runs the prompt itself (again, after a --dump pass) and then the tokens */
+        /* the device loop runs the prompt itself (again, after a --dump pass) and then the tokens,
+         * printing each id as it arrives */
         double ms[2] = {0.0, 0.0};
         int n = 0;
-        if (gen > 0 && !rbt_hip_generate(h, tokens, nt, gen, eos, ids, &n, ms)) goto done;
-        for (int g = 0; g < n; g++) printf("%d\n", ids[g]);
-        fflush(stdout);
+        if (gen > 0 && !rbt_hip_generate_stream(h, tokens, nt, gen, eos, print_token, NULL, ids, &n, ms)) goto done;
         produced = n;
         if (!dump_l) { /* the prompt/generation split of the device loop, from its HIP events */
             t1 = t0 + ms[0] * 1e-3;
-            t2 = t1 + ms[1] * 1e-3;
-        } else {
-            t2 = now_sec();
         }
+        t2 = t1 + ms[1] * 1e-3;
     }
     fprintf(stderr, "prompt: %d tokens in %.2fs (%.2f tok/s)", nt, t1 - t0, nt / (t1 - t0 + 1e-9));
     if (gen > 0) fprintf(stderr, " | generated %d in %.2fs (%.2f tok/s)", produced, t2 - t1, produced / (t2 - t1 + 1e-9));
     fprintf(stderr, "\n");
-    if (cache_stats) {
+    if (cache_budget) {
+        /* the forward() calls the engine makes: the prompt, then one per generated id but the last
+         * (rabbit2.c:704, :732-733) */
+        const int n_fwd = nt + (produced > 0 ? produced - 1 : 0);
+        const size_t per = (size_t)c->n_layers * c->top_k;
         uint64_t s[6];
-        if (!rbt_hip_expert_stats(h, s)) goto done;
+        hist = (int32_t *)malloc(sizeof(int32_t) * per * (size_t)n_fwd);
+        if (!hist) {
+            fprintf(stderr, "out of memory\n");
+            goto done;
+        }
+        if (!rbt_hip_routing_history(h, 0, 0, n_fwd, hist) ||
+            !rbt_hip_expert_cache_replay(cache_budget, expert_stride, c->n_layers, c->n_experts, c->top_k, hist,
+                                         (uint64_t)n_fwd, s))
+            goto done;
         fprintf(stderr,
                 "expert cache: hits=%llu misses=%llu evictions=%llu bytes_read=%llu resident_bytes=%llu "
                 "capacity_bytes=%llu\n",
@@ -133,6 +159,7 @@ done:
     free(logits);
     free(routing);
     free(ids);
+    free(hist);
     rbt_hip_free(h);
     return rc;
 }
@@ -197,7 +224,7 @@ int main(int argc, char **argv) {
         return 2;
     }
     int order = RBT_ORDER_SCALAR; /* the engine's default matvec (use_avx2 = 0, rabbit2.c:312) */
-    if (kernel) {
+    if (kernel) {                 /* rabbit2.c:652-661 */
         if (strcmp(kernel, "scalar") && strcmp(kernel, "auto") && strcmp(kernel, "avx2") && strcmp(kernel, "hip")) {
             fprintf(stderr, "--kernel must be scalar, auto, avx2 or hip\n");
             return 2;
@@ -206,7 +233,10 @@ int main(int argc, char **argv) {
             order = RBT_ORDER_AVX2;
         else if (strcmp(kernel, "scalar"))
             order = host_has_avx2() ? RBT_ORDER_AVX2 : RBT_ORDER_SCALAR;
-        fprintf(stderr, "matvec kernel: hip-gfx950 (router order %s)\n", order == RBT_ORDER_AVX2 ? "avx2" : "scalar");
+        if (!strcmp(kernel, "hip"))
+            fprintf(stderr, "matvec kernel: hip-gfx950 (router order %s)\n", order == RBT_ORDER_AVX2 ? "avx2" : "scalar");
+        else
+            fprintf(stderr, "matvec kernel: %s\n", order == RBT_ORDER_AVX2 ? "avx2" : "scalar");
     }
 
     rbt_config c;
@@ -242,8 +272,8 @@ int main(int argc, char **argv) {
             fprintf(stderr, "token %d out of range\n", tokens[i]);
             return 1;
         }
-    const int rc = run(argv[1], &c, order, ctx, tokens, nt, dump_l, dump_r, gen, eos, temperature, top_k_sample, top_p,
-                       seed, cache_mib != 0);
+    const int rc = run(argv[1], &c, inf[3], order, ctx, tokens, nt, dump_l, dump_r, gen, eos, temperature,
+                       top_k_sample, top_p, seed, cache_mib * 1024u * 1024u);
     free(tokens);
     return rc;
 }

@@ -153,14 +153,85 @@ def test_library_reports_file_info_without_a_device(tmp_path):
     import ctypes as C
     cfg, path = small_model(tmp_path, dtype=po.DT_F32, qk_norm=0)
     lib = hip.lib()
-    out_cfg = (C.c_int32 * 15)()
+    out_cfg = hip.Config()
     info = (C.c_uint64 * 7)()
-    assert lib.rbt_hip_file_info(os.fsencode(str(path)), out_cfg, info) == 1
+    assert lib.rbt_hip_file_info(os.fsencode(str(path)), C.byref(out_cfg), info) == 1
     lay = po.layout(cfg)
     assert list(info) == [lay["tok_emb"], lay["layers"][0]["experts"], lay["layers"][-1]["experts"],
                           lay["expert_stride"], lay["lm_head"], lay["end"], os.path.getsize(path)]
-    assert list(out_cfg)[:13] == [cfg.vocab, cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+    assert [getattr(out_cfg, f) for f, _ in hip.Config._fields_][:13] == [cfg.vocab, cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
                                   cfg.n_experts, cfg.top_k, cfg.expert_hidden, cfg.max_seq, cfg.dtype, cfg.qk_norm,
                                   cfg.norm_topk]
     assert lib.rbt_hip_file_info(os.fsencode(str(tmp_path / "none")), None, None) == 0
     assert b"cannot open" in lib.rbt_hip_last_error(None)
+
+
+def test_kernel_line_as_the_engine_prints_it(tmp_path):
+    """The reference's own check of the --kernel flag (rabbit2/tests/test_avx2.py:22-39) run against this
+    command line: --kernel auto prints 'matvec kernel: scalar|avx2', an invalid value fails, and --kernel
+    avx2 either prints 'matvec kernel: avx2' and succeeds or fails saying it is unavailable."""
+    import re
+    _, path = small_model(tmp_path)
+    for binary in [CLI] + ([po.REF_BIN] if po.have_ref() else []):
+        rc, _, err = run(binary, path, "--info", "--kernel", "auto")
+        assert rc == 0 and re.search(r"matvec kernel: (scalar|avx2)", err), (binary, err)
+        rc, _, err = run(binary, path, "--info", "--kernel", "invalid")
+        assert rc != 0, binary
+        rc, _, err = run(binary, path, "--info", "--kernel", "avx2")
+        if "matvec kernel: avx2" in err:
+            assert rc == 0, binary
+        else:
+            assert rc != 0 and "unavailable" in err, (binary, err)
+        rc, _, err = run(binary, path, "--info", "--kernel", "scalar")
+        assert rc == 0 and "matvec kernel: scalar" in err, (binary, err)
+    # the same choice as the engine's auto on this host
+    if po.have_ref():
+        assert run(CLI, path, "--info", "--kernel", "auto")[2] == run(po.REF_BIN, path, "--info", "--kernel", "auto")[2]
+    rc, _, err = run(CLI, path, "--info", "--kernel", "hip")
+    assert rc == 0 and "matvec kernel: hip-gfx950" in err
+
+
+def write_header(path, size, **over):
+    """A bare .rbt2 header of the given config fields, in a (sparse) file of `size` bytes."""
+    import struct
+    kw = dict(vocab=8, dim=8, n_layers=1, n_heads=2, n_kv_heads=2, head_dim=4, n_experts=2, top_k=1,
+              expert_hidden=8, max_seq=4, dtype=0, qk_norm=0, norm_topk=0)
+    kw.update(over)
+    hdr = b"RBT2" + struct.pack("<I13i2f", 2, *[kw[k] for k in ("vocab", "dim", "n_layers", "n_heads", "n_kv_heads",
+                                                                "head_dim", "n_experts", "top_k", "expert_hidden",
+                                                                "max_seq", "dtype", "qk_norm", "norm_topk")],
+                                1e4, 1e-5)
+    with open(path, "wb") as f:
+        f.write(hdr)
+        f.truncate(size)
+
+
+@pytest.mark.parametrize("over", [dict(n_layers=2**31 - 1), dict(vocab=2**31 - 1, dim=2**31 - 1, dtype=0),
+                                  dict(n_experts=2**31 - 1, expert_hidden=2**31 - 1, dim=2**31 - 1),
+                                  dict(n_heads=2**30, n_kv_heads=2**30, head_dim=2**30, dim=2**31 - 1)],
+                         ids=["layers", "vocab_dim", "experts", "heads"])
+def test_header_with_huge_fields_fails_cleanly(tmp_path, over):
+    """Header fields whose layout would run past 2^64 bytes or allocate a per-layer table the file
+    cannot back: a clean 'file too small' (exit 1), never an abort or a wrapped offset."""
+    path = tmp_path / "big.rbt2"
+    write_header(path, 1 << 20, **over)
+    rc, out, err = run(CLI, path, "--info")
+    assert rc == 1 and "file too small for its own config" in err, (rc, err)
+    from rabbitm2_amd import hip
+    import ctypes as C
+    assert hip.lib().rbt_hip_file_info(os.fsencode(str(path)), None, None) == 0
+    assert b"file too small" in hip.lib().rbt_hip_last_error(None)
+
+
+def test_file_too_small_reports_the_engine_end(tmp_path):
+    """A header whose layout ends past the file: the message carries the layout end exactly as the
+    engine computes it (rabbit2.c:221-225)."""
+    cfg, path = small_model(tmp_path)
+    end = po.layout(cfg)["end"]
+    with open(path, "r+b") as f:
+        f.truncate(end - 1)
+    rc, _, err = run(CLI, path, "--info")
+    assert rc == 1 and f"file too small for its own config ({end - 1} < {end})" in err
+    if po.have_ref():
+        rrc, _, rerr = run(po.REF_BIN, path, "--info")
+        assert rrc == 1 and f"({end - 1} < {end})" in rerr

@@ -226,3 +226,59 @@ def test_batch_arguments_checked(dev):
         dev.forward_batch([0, 0], [0, 8], cfg.vocab, cfg.n_layers, cfg.top_k)
     with pytest.raises(HipError):
         dev.generate_batch(np.zeros((2, 6), np.int32), 3)  # 6 + 3 > ctx 8
+
+
+def test_forward_batch_one_split_many_rounds(dev):
+    """32 sequences at the OLMoE head shape (16 heads x 128, QK-norm): 512 (sequence, head) blocks take one
+    position split each, and the attention kernel writes its output itself with no merge launch. Over 400
+    positions every wave of a block loops over up to 13 rounds of 8 positions. Sequences 0 and 31 are
+    checked against the oracle run on each alone at every position (routing identical, logits normwise
+    within 1e-3)."""
+    spec = MANIFEST["cases"]["olmoe_layer_bf16"]
+    cfg = po.Config(**dict(spec["config"], max_seq=512))
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    B, n = 32, 400
+    assert B * cfg.n_heads >= 512  # the one-split attention (kAttnDirectBlocks)
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, n, seed=41)
+    want = {b: po.run(model, prompts[b], order=po.ORDER_AVX2, ctx=n) for b in (0, B - 1)}
+    dev.batch_init(B, n)
+    for p in range(n):
+        logits, routing = dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
+                                            cfg.top_k)
+        for b, (wl, wr, _) in want.items():
+            assert np.array_equal(routing[:, b, :], wr[p]), f"seq {b} pos {p}"
+            err = normwise_err(logits[b], wl[p])
+            assert err <= LOGIT_RTOL, f"seq {b} pos {p}: logits error {err:.2e}"
+
+
+def test_deferred_profile_on_the_fused_combine_path(dev):
+    """Deferred profiling (mode 2) of batched steps whose combine runs fused with the next RMSNorm: every
+    event pair taken is recorded, so every kernel kind reads back, and the timed steps still match the
+    oracle."""
+    spec, cfg, model = build("olmoe_layer_bf16")
+    B = 16
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    prompts = prompts_for(cfg, B, 2, seed=5)
+    dev.batch_init(B, 0)
+    dev.profile(2)
+    try:
+        outs = [dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers, cfg.top_k)
+                for p in range(2)]
+        counts = {}
+        for name in ("router", "topk", "dispatch", "gateup", "down_combine", "combine", "qkv", "attention", "wo",
+                     "lm_head"):
+            ms, launches = dev.profile_get(name)
+            counts[name] = launches
+            assert launches == 0 or ms > 0, name
+        assert counts["combine"] == 2 and counts["gateup"] == 2, counts
+    finally:
+        dev.profile(0)
+    wl, wr, _ = po.run(model, prompts[0], order=po.ORDER_AVX2)
+    for p in range(2):
+        assert np.array_equal(outs[p][1][:, 0, :], wr[p])
+        assert normwise_err(outs[p][0][0], wl[p]) <= LOGIT_RTOL

@@ -24,6 +24,8 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 MANIFEST = json.load(open(os.path.join(GOLDEN, "manifest.json")))["cases"]
 SAMPLED = json.load(open(os.path.join(GOLDEN, "sampled.json")))
 KERNEL_FLAGS = {"scalar": [], "avx2": ["--kernel", "avx2"]}  # the orders the fixtures were written in
+CACHE = json.load(open(os.path.join(GOLDEN, "cache_stats.json")))
+STATS_RE = re.compile(r"(hits|misses|evictions|bytes_read|resident_bytes|capacity_bytes)=(\d+)")
 LOGIT_RTOL = 1e-3
 
 
@@ -91,11 +93,81 @@ def test_cli_eos_ctx_and_expert_cache_line(tmp_path):
     out, err = run(path, "--dump", lp, rp, "--gen", spec["n_gen"], "--expert-cache-mib", 64, *tokens)
     assert [int(v) for v in out.split()] == full
     assert np.array_equal(np.fromfile(rp, dtype="<i4").reshape(fx["routing_scalar"].shape), fx["routing_scalar"])
-    stats = {k: int(v) for k, v in re.findall(r"(hits|misses|evictions|bytes_read|resident_bytes|capacity_bytes)=(\d+)",
-                                              err)}
+    stats = {k: int(v) for k, v in STATS_RE.findall(err)}
     stride = po.layout(cfg)["expert_stride"]
-    assert stats["misses"] == cfg.n_layers * cfg.n_experts and stats["evictions"] == 0
-    assert stats["bytes_read"] == stats["misses"] * stride
-    assert stats["hits"] > 0
+    assert stats["evictions"] == 0 and stats["bytes_read"] == stats["misses"] * stride
+    assert stats["hits"] + stats["misses"] == (len(tokens) + len(full) - 1) * cfg.n_layers * cfg.top_k
     out, err = run(path, "--gen", 2, "--kernel", "hip", *tokens)
     assert "matvec kernel: hip-gfx950" in err and len(out.split()) == 2
+
+
+@pytest.mark.parametrize("case", sorted({r["case"] for r in CACHE["runs"]}))
+def test_cli_expert_cache_line_matches_engine(tmp_path, case):
+    """--expert-cache-mib as the reference's cache test runs it (rabbit2/tests/test_engine_cache.py:23-57):
+    the dump files identical with and without a budget, and the stats line equal to the reference
+    engine's own for the same arguments (tests/golden/cache_stats.json) -- evictions at small budgets,
+    resident_bytes within the budget, bytes_read == misses * expert_stride."""
+    spec, cfg, path = write_case(case, tmp_path)
+    stride = po.layout(cfg)["expert_stride"]
+    runs = [r for r in CACHE["runs"] if r["case"] == case]
+    lp, rp = tmp_path / "l.bin", tmp_path / "r.bin"
+    plain = {}
+    for tag, flags in KERNEL_FLAGS.items():
+        run(path, "--dump", lp, rp, *flags, *runs[0]["tokens"])
+        plain[tag] = (lp.read_bytes(), rp.read_bytes())
+    for r in runs:
+        flags = KERNEL_FLAGS[r["order"]]
+        _, err = run(path, "--dump", lp, rp, "--expert-cache-mib", r["budget_mib"], *flags, *r["tokens"])
+        assert rp.read_bytes() == plain[r["order"]][1]
+        assert np.array_equal(np.fromfile(lp, "<f4"), np.frombuffer(plain[r["order"]][0], "<f4"))
+        stats = {k: int(v) for k, v in STATS_RE.findall(err)}
+        assert stats == r["dump"], (r["order"], r["budget_mib"], stats)
+        assert stats["resident_bytes"] <= r["budget_mib"] * 1024 * 1024
+        assert stats["bytes_read"] == stats["misses"] * stride
+        out, err = run(path, "--gen", r["n_gen"], "--expert-cache-mib", r["budget_mib"], *flags, *r["tokens"])
+        assert [int(t) for t in out.split()] == r["gen_ids"]
+        stats = {k: int(v) for k, v in STATS_RE.findall(err)}
+        assert stats == r["gen"], (r["order"], r["budget_mib"], "gen", stats)
+    small = min(r["budget_mib"] for r in runs)
+    if any(r["dump"]["evictions"] for r in runs if r["budget_mib"] == small):
+        print(f"{case}: evictions at {small} MiB as the engine's", flush=True)
+
+
+def test_cli_gen_prints_each_id_on_its_own_line(tmp_path):
+    """--gen writes one id per line as the engine does (rabbit2.c:728-729), read here line by line from
+    the pipe as the reference's server does (rabbit2/tools/serve.py:45-60)."""
+    spec, cfg, path = write_case("tiny_olmoe_bf16", tmp_path)
+    fx = np.load(os.path.join(GOLDEN, "tiny_olmoe_bf16.npz"))
+    tokens = [str(int(t)) for t in fx["tokens"]]
+    proc = subprocess.Popen([CLI, str(path), "--gen", str(spec["n_gen"]), "--kernel", "avx2"] + tokens,
+                            stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, bufsize=1)
+    ids = []
+    for line in proc.stdout:
+        assert line.endswith("\n") and line.strip().lstrip("-").isdigit(), repr(line)
+        ids.append(int(line))
+    err = proc.stderr.read()
+    assert proc.wait(timeout=120) == 0, err
+    assert ids == fx["gen_avx2"].tolist()
+
+
+def test_generate_stream_reports_ids_in_order(dev):
+    """rbt_hip_generate_stream: the callback sees the device loop's ids in order; the eos id is reported
+    and ends the output; a callback returning 0 stops it; out and n_out as rbt_hip_generate."""
+    spec, cfg, _ = MANIFEST["tiny_olmoe_f32"], po.Config(**MANIFEST["tiny_olmoe_f32"]["config"]), None
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    fx = np.load(os.path.join(GOLDEN, "tiny_olmoe_f32.npz"))
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    dev.state_init(0)
+    want = fx["gen_avx2"].tolist()
+    seen, out, ms = dev.generate_stream(fx["tokens"], spec["n_gen"])
+    assert seen == want and out == want and ms[1] > 0
+    eos = want[20]
+    seen, out, _ = dev.generate_stream(fx["tokens"], spec["n_gen"], eos=eos)
+    assert seen == want[:want.index(eos) + 1] and out == seen
+    seen, out, _ = dev.generate_stream(fx["tokens"], spec["n_gen"], stop_after=5)
+    assert seen == want[:5] and out == want[:5]
+    ids, _ = dev.generate(fx["tokens"], spec["n_gen"])  # the plain loop after a stopped stream
+    assert ids == want

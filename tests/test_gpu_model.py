@@ -67,3 +67,51 @@ def test_upload_rejects_bad_images(dev):
     bad[8 + 7 * 4: 8 + 8 * 4] = np.frombuffer(np.int32(99).tobytes(), np.uint8)  # top_k > n_experts
     with pytest.raises(HipError, match="invalid config"):
         dev.upload(bad)
+
+
+def test_rejected_upload_keeps_the_loaded_model(dev, tmp_path):
+    """A header that fails load_model's checks (rabbit2.c:199-228) leaves the handle's model and decode
+    state as they were: the forward pass started before the rejected uploads continues at the next
+    positions with the reference's routing and logits (the golden fixture of ref_bf16)."""
+    import json
+    import os
+    import struct
+    from rabbitm2_amd.hip import HipError
+    from tests.common import normwise_err as nerr
+    here = os.path.dirname(os.path.abspath(__file__))
+    spec = json.load(open(os.path.join(here, "golden", "manifest.json")))["cases"]["ref_bf16"]
+    cfg = po.Config(**spec["config"])
+    g = spec["gen_params"]
+    model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
+                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
+    fx = np.load(os.path.join(here, "golden", "ref_bf16.npz"))
+    dev.upload(model)
+    dev.set_router_order(po.ORDER_AVX2)
+    dev.state_init(0)
+    tokens = fx["tokens"]
+
+    def step(pos):
+        logits, routing = dev.forward(int(tokens[pos]), pos, cfg.vocab, cfg.n_layers, cfg.top_k)
+        assert np.array_equal(routing, fx["routing_avx2"][pos]), pos
+        assert nerr(logits, fx["logits_avx2"][pos]) <= 1e-3, pos
+
+    half = len(tokens) // 2
+    for pos in range(half):
+        step(pos)
+    other = po.build_model(po.Config(dtype=po.DT_F32, dim=128, n_layers=3), po.ref_style(7))
+    bad_magic = other.copy()
+    bad_magic[0] = ord("X")
+    huge = other.copy()  # n_layers = 2^31 - 1: the layout runs past the image
+    huge[8 + 2 * 4: 8 + 3 * 4] = np.frombuffer(struct.pack("<i", 2**31 - 1), np.uint8)
+    wrapped = other.copy()  # vocab * dim * 4 bytes past 2^64
+    wrapped[8: 8 + 2 * 4] = np.frombuffer(struct.pack("<ii", 2**31 - 1, 2**31 - 1), np.uint8)
+    for img, msg in ((bad_magic, "bad magic"), (other[: other.size // 3], "too small"), (huge, "too small"),
+                     (wrapped, "too small")):
+        with pytest.raises(HipError, match=msg):
+            dev.upload(img)
+    short = tmp_path / "short.rbt2"
+    other[: other.size // 3].tofile(short)
+    with pytest.raises(HipError, match="too small"):
+        dev.upload_file(str(short))
+    for pos in range(half, len(tokens)):
+        step(pos)
