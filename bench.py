@@ -188,7 +188,8 @@ def main():
     # ---- per-kernel durations of the step: HIP events around every launch (deferred profiling, nothing
     # waits between launches) in eager forward() steps at the generated positions
     dev.state_init(ctx)
-    seq = prompt.tolist() + ids
+    seq = prompt.tolist() + ids  # the timed run's tokens, padded with random ids for short runs
+    seq += np.random.default_rng(SEED + 1).integers(0, cfg.vocab, max(0, N_PROMPT + PROFILE_STEPS - len(seq))).tolist()
     for pos in range(N_PROMPT):
         dev.forward(seq[pos], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
     dev.profile(2)

@@ -153,6 +153,7 @@ struct FaultPlan {
 };
 
 int fault_kind(const char *call) {
+    while (*call == '(' || *call == ' ') call++;  // launch macros pass their call parenthesised
     if (strstr(call, "hipMalloc") || strstr(call, "hipHostMalloc")) return 0;
     if (strncmp(call, "launch_", 7) == 0) return 1;
     if (strstr(call, "hipMemcpy")) return 2;
@@ -191,11 +192,18 @@ int fail(rbt_hip *h, const char *fmt, ...) {
         if (e_ != hipSuccess) return fail((h), "%s failed: %s", #call, hipGetErrorString(e_)); \
     } while (0)
 
-// A HIP call whose error the caller handles itself, with the same fault injection point.
-#define HIP_TRY(call)                                    \
-    ([&]() -> hipError_t {                               \
-        const hipError_t f_ = fault_point(#call);        \
-        return f_ != hipSuccess ? f_ : (call);           \
+// A HIP call whose error the caller handles itself, with the same fault injection point; the text of
+// the last such call that failed is kept for the caller's message (failed_call()).
+thread_local const char *g_failed_call = "";
+hipError_t note_call(hipError_t e, const char *call) {
+    if (e != hipSuccess) g_failed_call = call;
+    return e;
+}
+const char *failed_call() { return g_failed_call; }
+#define HIP_TRY(call)                                                      \
+    ([&]() -> hipError_t {                                                 \
+        const hipError_t f_ = fault_point(#call);                          \
+        return note_call(f_ != hipSuccess ? f_ : (call), #call);           \
     }())
 
 int set_device(rbt_hip *h) {
@@ -1378,16 +1386,16 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
     }
     hipError_t e = hipSuccess;
     for (int i = 0; i < 3 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
-    if (e == hipSuccess) e = hipEventRecord(ev[0], h->stream);
+    if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[0], h->stream));
     // the prompt: n_prompt forwards, the last one with lm_head + argmax (the first generated token)
     for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = HIP_TRY(hipGraphLaunch(g_adv, h->stream));
     int n = n_gen;
     if (!on_token) {
         if (e == hipSuccess && n_gen > 0) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
-        if (e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
+        if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[1], h->stream));
         // each further token: one forward of the previous one (rabbit2.c:733)
         for (int g = 1; g < n_gen && e == hipSuccess; g++) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
-        if (e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+        if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
         if (e == hipSuccess && n_gen > 0)
             e = HIP_TRY(hipMemcpyAsync(out, h->ds.seq + n_prompt, 4 * (size_t)n_gen, hipMemcpyDeviceToHost, h->stream));
         if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
@@ -1402,11 +1410,11 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
         bool more = n_gen > 0, report = true;
         auto queue_step = [&](int g) -> hipError_t {
             hipError_t r = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
-            if (r == hipSuccess && g == 0) r = hipEventRecord(ev[1], h->stream);
+            if (r == hipSuccess && g == 0) r = HIP_TRY(hipEventRecord(ev[1], h->stream));
             if (r == hipSuccess)
                 r = HIP_TRY(hipMemcpyAsync(h->tok_host + g, h->ds.seq + n_prompt + g, 4, hipMemcpyDeviceToHost,
                                            h->stream));
-            if (r == hipSuccess) r = hipEventRecord(ring[g % kStreamAhead], h->stream);
+            if (r == hipSuccess) r = HIP_TRY(hipEventRecord(ring[g % kStreamAhead], h->stream));
             return r;
         };
         n = 0;
@@ -1414,7 +1422,7 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
             while (e == hipSuccess && more && queued < reported + kStreamAhead) {
                 e = queue_step(queued++);
                 if (queued == n_gen) more = false;
-                if (!more && e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+                if (!more && e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
             }
             if (e != hipSuccess || reported == queued) break;
             e = HIP_TRY(hipEventSynchronize(ring[reported % kStreamAhead]));
@@ -1426,25 +1434,25 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
             if (tok == eos || !report) {  // nothing more is queued; the queued steps run to their end
                 if (more) {
                     more = false;
-                    e = hipEventRecord(ev[2], h->stream);
+                    e = HIP_TRY(hipEventRecord(ev[2], h->stream));
                 }
                 break;
             }
         }
         if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
-        if (n_gen == 0 && e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
-        if (n_gen == 0 && e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+        if (n_gen == 0 && e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[1], h->stream));
+        if (n_gen == 0 && e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
         if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
     }
     if (e == hipSuccess && ms_out) {
         float a = 0.0f, b = 0.0f;
-        e = hipEventElapsedTime(&a, ev[0], ev[1]);
-        if (e == hipSuccess) e = hipEventElapsedTime(&b, ev[1], ev[2]);
+        e = HIP_TRY(hipEventElapsedTime(&a, ev[0], ev[1]));
+        if (e == hipSuccess) e = HIP_TRY(hipEventElapsedTime(&b, ev[1], ev[2]));
         ms_out[0] = a;
         ms_out[1] = b;
     }
     cleanup();
-    if (e != hipSuccess) return fail(h, "generate: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(h, "generate: %s failed: %s", failed_call(), hipGetErrorString(e));
     if (n_out) *n_out = n;
     return 1;
 }
@@ -1508,21 +1516,21 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
     h->prof.mode = prof;
     hipError_t e = hipSuccess;
     if (ok) {
-        for (int i = 0; i < 3 && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);
-        if (e == hipSuccess) e = hipEventRecord(ev[0], h->stream);
-        for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = hipGraphLaunch(g_adv, h->stream);
-        if (e == hipSuccess && n_gen > 0) e = hipGraphLaunch(g_fin, h->stream);
-        if (e == hipSuccess) e = hipEventRecord(ev[1], h->stream);
-        for (int g = 1; g < n_gen && e == hipSuccess; g++) e = hipGraphLaunch(g_fin, h->stream);
-        if (e == hipSuccess) e = hipEventRecord(ev[2], h->stream);
+        for (int i = 0; i < 3 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
+        if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[0], h->stream));
+        for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = HIP_TRY(hipGraphLaunch(g_adv, h->stream));
+        if (e == hipSuccess && n_gen > 0) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[1], h->stream));
+        for (int g = 1; g < n_gen && e == hipSuccess; g++) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
         for (int b = 0; b < B && e == hipSuccess && n_gen > 0; b++)
-            e = hipMemcpyAsync(out + (size_t)b * n_gen, h->ds.seq + (size_t)b * ctx + n_prompt, 4 * (size_t)n_gen,
-                               hipMemcpyDeviceToHost, h->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+            e = HIP_TRY(hipMemcpyAsync(out + (size_t)b * n_gen, h->ds.seq + (size_t)b * ctx + n_prompt,
+                                       4 * (size_t)n_gen, hipMemcpyDeviceToHost, h->stream));
+        if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
         if (e == hipSuccess && ms_out) {
             float a = 0.0f, bms = 0.0f;
-            e = hipEventElapsedTime(&a, ev[0], ev[1]);
-            if (e == hipSuccess) e = hipEventElapsedTime(&bms, ev[1], ev[2]);
+            e = HIP_TRY(hipEventElapsedTime(&a, ev[0], ev[1]));
+            if (e == hipSuccess) e = HIP_TRY(hipEventElapsedTime(&bms, ev[1], ev[2]));
             ms_out[0] = a;
             ms_out[1] = bms;
         }
@@ -1532,7 +1540,7 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
     for (hipEvent_t ei : ev)
         if (ei) (void)hipEventDestroy(ei);
     if (!ok) return 0;
-    if (e != hipSuccess) return fail(h, "generate_batch: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(h, "generate_batch: %s failed: %s", failed_call(), hipGetErrorString(e));
     return 1;
 }
 
