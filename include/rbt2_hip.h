@@ -124,6 +124,17 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
                     int32_t *routing_dev, float *weights_dev);
 int rbt_hip_reserve(rbt_hip *h, const rbt_moe_layer *L, int max_tokens);
 
+/* rbt_hip_moe_dev that allocates nothing (no counterpart in the reference; for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, hosts that forbid it).
+ * Same arguments, kernels and results as rbt_hip_moe_dev, but the workspace is a fixed 64 MiB scratch
+ * array the library holds on each GPU until the process ends, instead of the handle's workspace: calls
+ * whose workspace would exceed it fail with a message (a 512-token call at the OLMoE layer shape needs
+ * 52.2 MiB). No profiling events are taken. Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other handles, other streams, other threads) race; calls on one stream run
+ * in order. rbt_hip_expert_counts_dev then points into the array until the next call. */
+int rbt_hip_moe_dev_noalloc(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, float *x_dev,
+                            float *moe_dev, int32_t *routing_dev, float *weights_dev);
+
 /* Tokens-per-expert histogram of the last rbt_hip_moe_dev call that used the grouped (prefill)
  * path, [n_experts] int32, device pointer owned by the handle; NULL if none. */
 const int32_t *rbt_hip_expert_counts_dev(rbt_hip *h);

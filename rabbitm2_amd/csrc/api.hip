@@ -7,6 +7,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include <fcntl.h>
@@ -18,6 +19,8 @@
 
 using namespace rbt;
 
+static __device__ __align__(256) uint8_t scratch[64u << 20];  // see kScratchBytes
+
 namespace {
 
 constexpr uint64_t kAlign = 4096;  // rabbit2.c:56
@@ -28,6 +31,15 @@ constexpr int kMaxTopK = 64;       // rabbit2.c:59
 constexpr uint64_t kMaxImageBytes = 1ull << 50;
 
 char g_init_err[512];
+
+// Scratch of rbt_hip_moe_dev_noalloc: one array per GPU, for callers that cannot allocate. 64 MiB holds
+// the workspace of a 512-token call at the OLMoE layer shape (52.2 MiB). Host code never uses the
+// array's name as an address: rbt_hip_init looks up each device's own copy (hipGetSymbolAddress) once,
+// with that device current, and every launch takes that address.
+constexpr size_t kScratchBytes = 64u << 20;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
 
 struct LayerOff {
     uint64_t attn_norm, wq, wk, wv, wo, q_norm, k_norm, ffn_norm, router, experts;
@@ -122,6 +134,8 @@ struct rbt_hip {
     // pinned host ring the streaming generate reads tokens from
     int32_t *tok_host = nullptr;
     int tok_host_n = 0;
+    // this device's scratch array (rbt_hip_moe_dev_noalloc), from hipGetSymbolAddress at init
+    void *scratch = nullptr;
     // expert residency counters in the engine's cache-stats terms (rabbit2.c:745-751): every expert is
     // read from the file once at upload (a miss) and every later use of a selected expert is a hit
     uint64_t cache_hits = 0, cache_misses = 0;
@@ -402,6 +416,8 @@ Launch lc(rbt_hip *h, int k) {
     }
     return L;
 }
+
+Launch lc_timed(rbt_hip *h, int k) { return lc(h, k); }
 
 // Mode 1: waits for the call's events and adds each bracketed kernel's duration.
 int prof_collect(rbt_hip *h) {
@@ -695,6 +711,124 @@ int capture_step(rbt_hip *h, bool final, hipGraphExec_t *exec) {
     return 1;
 }
 
+// The form the MoE block takes for a call: the batch-1 kernels with the top-k inside gate/up, the
+// grouped GEMM path, or the per-pair GEMVs. (Both workspaces give the h buffer 256-byte alignment, so
+// the decode kernels' alignment test sees xb's, which it also checks.)
+enum MoeForm { kMoeFastDecode, kMoeGrouped, kMoeGeneral };
+MoeForm moe_form(const rbt_hip *h, const rbt_moe_layer *L, int T, const float *xb) {
+    if (T == 1 && h->fused_decode && L->n_experts <= kTopkInGateupMaxE &&
+        experts_decode_supported(L->dtype, T, L->top_k, L->dim, L->expert_hidden, L->experts, L->expert_stride, xb,
+                                 xb))
+        return kMoeFastDecode;
+    if (prefill_supported(L->dtype, T, h->prefill_min_tokens, L->n_experts, L->top_k, L->dim, L->expert_hidden,
+                          L->experts, L->expert_stride, xb))
+        return kMoeGrouped;
+    return kMoeGeneral;
+}
+
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Scratch bytes of one MoE call: probs [T][E], routing and weights [T][K], hbuf [T*K][H], and the
+// grouped path's lists, down outputs and activation planes.
+size_t moe_scratch_bytes(int T, int E, int K, int H, int D, bool grouped) {
+    const size_t t = (size_t)T;
+    return up256(4 * t * E) + 2 * up256(4 * t * K) + up256(4 * t * K * H) +
+           (grouped ? prefill_workspace_bytes(T, E, K, D) : 0);
+}
+
+// A workspace view of the scratch array (device address `base`), in moe_scratch_bytes' order.
+Workspace scratch_view(void *base, int T, int E, int K, int H, int D, bool grouped) {
+    uint8_t *p = static_cast<uint8_t *>(base);
+    const size_t t = (size_t)T;
+    Workspace w;
+    w.tokens = T;
+    w.E = E;
+    w.K = K;
+    w.H = H;
+    w.probs = reinterpret_cast<float *>(p);
+    p += up256(4 * t * E);
+    w.routing = reinterpret_cast<int32_t *>(p);
+    p += up256(4 * t * K);
+    w.weights = reinterpret_cast<float *>(p);
+    p += up256(4 * t * K);
+    w.hbuf = reinterpret_cast<float *>(p);
+    p += up256(4 * t * K * H);
+    w.pre = grouped ? p : nullptr;
+    w.pre_bytes = grouped ? prefill_workspace_bytes(T, E, K, D) : 0;
+    return w;
+}
+
+// The MoE block (rabbit2.c:513-542) on a workspace w sized for this call by the caller: probs, routing,
+// weights, hbuf, and for the grouped form pre. timed: launches take profiling events (the handle
+// workspace path); the scratch path takes none.
+int moe_block(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, float *x_dev, float *moe_dev,
+              int32_t *routing_dev, float *weights_dev, Workspace &w, MoeForm form, bool timed) {
+    auto lc = [timed](rbt_hip *hh, int k) {
+        if (timed) return lc_timed(hh, k);
+        Launch plain;
+        plain.s = hh->stream;
+        return plain;
+    };
+    int32_t *routing = routing_dev ? routing_dev : w.routing;
+    float *weights = weights_dev ? weights_dev : w.weights;
+    const bool decode_kernels = experts_decode_supported(L->dtype, T, L->top_k, L->dim, L->expert_hidden, L->experts,
+                                                         L->expert_stride, xb_dev, w.hbuf);
+    auto done = [&]() { return timed ? prof_collect(h) : 1; };
+    if (form == kMoeFastDecode) {
+        // batch 1: router logits, then gate/up (with the top-k in every block), then down + combine
+        HIP_OK(h, launch_router_logits(lc(h, kProfRouter), h->order, L->dtype, xb_dev, L->router, L->router_bias, T,
+                                       L->n_experts, L->dim, w.probs));
+        HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
+                                        routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
+                                        moe_dev, w.probs, L->n_experts, L->norm_topk));
+        return done();
+    }
+    if (form == kMoeGrouped) {
+        // router, top-k and the activation split in one launch when it applies, else the two router
+        // kernels (the grouped path then splits the activations itself)
+        const bool fused = router_prefill_supported(h->order, L->dtype, T, L->n_experts, L->dim, L->top_k,
+                                                    L->router, xb_dev);
+        if (fused && T <= kRouterDecodeMaxT) {  // few tokens: decode router kernel, then top-k + split
+            uint16_t *x_hi = nullptr, *x_lo = nullptr;
+            prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
+            HIP_OK(h, launch_router_logits(lc(h, kProfRouter), h->order, L->dtype, xb_dev, L->router, L->router_bias, T,
+                                           L->n_experts, L->dim, w.probs));
+            HIP_OK(h, launch_topk_split(lc(h, kProfTopk), w.probs, T, L->n_experts, L->top_k, L->norm_topk, xb_dev, L->dim,
+                                        routing, weights, x_hi, x_lo));
+        } else if (fused) {
+            uint16_t *x_hi = nullptr, *x_lo = nullptr;
+            prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
+            HIP_OK(h, launch_router_prefill(lc(h, kProfRouter), L->dtype, xb_dev, L->router, L->router_bias, T,
+                                            L->n_experts, L->dim, L->top_k, L->norm_topk, routing, weights, x_hi,
+                                            x_lo));
+        } else {
+            HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
+                                    L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs,
+                                    routing, weights));
+        }
+        int32_t *counts = nullptr;
+        HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
+                                 L->experts, L->expert_stride, xb_dev, T, L->n_experts, L->top_k, L->dim,
+                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts, fused));
+        h->expert_counts = counts;
+        return done();
+    }
+    HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
+                            L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
+                            weights));
+    if (decode_kernels) {
+        HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
+                                        routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
+                                        moe_dev, nullptr, L->n_experts, L->norm_topk));
+    } else {
+        HIP_OK(h, launch_gateup_gemv(lc(h, kProfGateup), L->dtype, L->experts, L->expert_stride, routing, xb_dev, T,
+                                     L->top_k, L->dim, L->expert_hidden, w.hbuf));
+        HIP_OK(h, launch_down_combine(lc(h, kProfDown), L->dtype, L->experts, L->expert_stride, routing, weights,
+                                      w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev, moe_dev));
+    }
+    return done();
+}
+
 }  // namespace
 
 extern "C" {
@@ -706,6 +840,7 @@ int rbt_hip_init(rbt_hip **out, int device) {
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n == 0) return fail(nullptr, "init: no HIP device (%s)", hipGetErrorString(e));
     if (device < 0 || device >= n) return fail(nullptr, "init: device %d out of range (have %d)", device, n);
+    if (device >= kMaxDevices) return fail(nullptr, "init: device %d beyond the %d supported", device, kMaxDevices);
     rbt_hip *h = new rbt_hip();
     h->device = device;
     e = hipSetDevice(device);
@@ -714,6 +849,21 @@ int rbt_hip_init(rbt_hip **out, int device) {
         fail(nullptr, "init: %s", hipGetErrorString(e));
         delete h;
         return 0;
+    }
+    {  // the scratch array's address on this device, looked up once per device with the device current
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (!g_scratch_ptr[device]) {
+            void *p = nullptr;
+            e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p) {
+                fail(nullptr, "init: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+                (void)hipStreamDestroy(h->stream);
+                delete h;
+                return 0;
+            }
+            g_scratch_ptr[device] = p;
+        }
+        h->scratch = g_scratch_ptr[device];
     }
     *out = h;
     return 1;
@@ -939,66 +1089,27 @@ int rbt_hip_moe_dev(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int
     if (!xb_dev) return fail(h, "moe: xb is NULL");
     if (!set_device(h)) return 0;
     if (!ws_reserve(h, T, L->n_experts, L->top_k, L->expert_hidden)) return 0;
-    Workspace &w = h->ws;
-    int32_t *routing = routing_dev ? routing_dev : w.routing;
-    float *weights = weights_dev ? weights_dev : w.weights;
-    const bool decode_kernels = experts_decode_supported(L->dtype, T, L->top_k, L->dim, L->expert_hidden, L->experts,
-                                                         L->expert_stride, xb_dev, w.hbuf);
-    if (decode_kernels && h->fused_decode && T == 1 && L->n_experts <= kTopkInGateupMaxE) {
-        // batch 1: router logits, then gate/up (with the top-k in every block), then down + combine
-        HIP_OK(h, launch_router_logits(lc(h, kProfRouter), h->order, L->dtype, xb_dev, L->router, L->router_bias, T,
-                                       L->n_experts, L->dim, w.probs));
-        HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
-                                        routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
-                                        moe_dev, w.probs, L->n_experts, L->norm_topk));
-        return prof_collect(h);
-    }
-    if (prefill_supported(L->dtype, T, h->prefill_min_tokens, L->n_experts, L->top_k, L->dim, L->expert_hidden,
-                          L->experts, L->expert_stride, xb_dev)) {
-        if (!pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim))) return 0;
-        // router, top-k and the activation split in one launch when it applies, else the two router
-        // kernels (the grouped path then splits the activations itself)
-        const bool fused = router_prefill_supported(h->order, L->dtype, T, L->n_experts, L->dim, L->top_k,
-                                                    L->router, xb_dev);
-        if (fused && T <= kRouterDecodeMaxT) {  // few tokens: decode router kernel, then top-k + split
-            uint16_t *x_hi = nullptr, *x_lo = nullptr;
-            prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
-            HIP_OK(h, launch_router_logits(lc(h, kProfRouter), h->order, L->dtype, xb_dev, L->router, L->router_bias, T,
-                                           L->n_experts, L->dim, w.probs));
-            HIP_OK(h, launch_topk_split(lc(h, kProfTopk), w.probs, T, L->n_experts, L->top_k, L->norm_topk, xb_dev, L->dim,
-                                        routing, weights, x_hi, x_lo));
-        } else if (fused) {
-            uint16_t *x_hi = nullptr, *x_lo = nullptr;
-            prefill_x_planes(w.pre, T, L->n_experts, L->top_k, L->dim, &x_hi, &x_lo);
-            HIP_OK(h, launch_router_prefill(lc(h, kProfRouter), L->dtype, xb_dev, L->router, L->router_bias, T,
-                                            L->n_experts, L->dim, L->top_k, L->norm_topk, routing, weights, x_hi,
-                                            x_lo));
-        } else {
-            HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
-                                    L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs,
-                                    routing, weights));
-        }
-        int32_t *counts = nullptr;
-        HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
-                                 L->experts, L->expert_stride, xb_dev, T, L->n_experts, L->top_k, L->dim,
-                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts, fused));
-        h->expert_counts = counts;
-        return prof_collect(h);
-    }
-    HIP_OK(h, launch_router(lc(h, kProfRouter), lc(h, kProfTopk), h->order, L->dtype, xb_dev, L->router,
-                            L->router_bias, T, L->n_experts, L->dim, L->top_k, L->norm_topk, w.probs, routing,
-                            weights));
-    if (decode_kernels) {
-        HIP_OK(h, launch_experts_decode(lc(h, kProfGateup), lc(h, kProfDown), L->dtype, L->experts, L->expert_stride,
-                                        routing, weights, xb_dev, w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev,
-                                        moe_dev, nullptr, L->n_experts, L->norm_topk));
-    } else {
-        HIP_OK(h, launch_gateup_gemv(lc(h, kProfGateup), L->dtype, L->experts, L->expert_stride, routing, xb_dev, T,
-                                     L->top_k, L->dim, L->expert_hidden, w.hbuf));
-        HIP_OK(h, launch_down_combine(lc(h, kProfDown), L->dtype, L->experts, L->expert_stride, routing, weights,
-                                      w.hbuf, T, L->top_k, L->dim, L->expert_hidden, x_dev, moe_dev));
-    }
-    return prof_collect(h);
+    const MoeForm form = moe_form(h, L, T, xb_dev);
+    if (form == kMoeGrouped && !pre_reserve(h, prefill_workspace_bytes(T, L->n_experts, L->top_k, L->dim))) return 0;
+    return moe_block(h, L, xb_dev, T, x_dev, moe_dev, routing_dev, weights_dev, h->ws, form, true);
+}
+
+int rbt_hip_moe_dev_noalloc(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, float *x_dev,
+                            float *moe_dev, int32_t *routing_dev, float *weights_dev) {
+    if (!h) return fail(nullptr, "moe_noalloc: handle is NULL");
+    if (T < 0) return fail(h, "moe_noalloc: negative token count");
+    if (!check_layer(h, L)) return 0;
+    if (T == 0) return 1;
+    if (!xb_dev) return fail(h, "moe_noalloc: xb is NULL");
+    if (!h->scratch) return fail(h, "moe_noalloc: no scratch address for device %d", h->device);
+    const MoeForm form = moe_form(h, L, T, xb_dev);
+    const size_t need = moe_scratch_bytes(T, L->n_experts, L->top_k, L->expert_hidden, L->dim, form == kMoeGrouped);
+    if (need > kScratchBytes)
+        return fail(h, "moe_noalloc: %d tokens of this layer need %zu bytes of scratch, above its %zu bytes", T, need,
+                    (size_t)kScratchBytes);
+    if (!set_device(h)) return 0;
+    Workspace w = scratch_view(h->scratch, T, L->n_experts, L->top_k, L->expert_hidden, L->dim, form == kMoeGrouped);
+    return moe_block(h, L, xb_dev, T, x_dev, moe_dev, routing_dev, weights_dev, w, form, false);
 }
 
 const int32_t *rbt_hip_expert_counts_dev(rbt_hip *h) { return h ? h->expert_counts : nullptr; }

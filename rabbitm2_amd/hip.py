@@ -24,6 +24,7 @@ EXPORTS = (
     "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
     "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling", "rbt_hip_file_info",
     "rbt_hip_generate_stream", "rbt_hip_routing_history", "rbt_hip_expert_cache_replay",
+    "rbt_hip_moe_dev_noalloc",
 )
 
 TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32)
@@ -65,6 +66,7 @@ def lib():
         L.rbt_hip_layer.argtypes = [vp, i32, C.POINTER(MoeLayer)]
         L.rbt_hip_moe.argtypes = [vp, i32, vp, i32, vp, vp]
         L.rbt_hip_moe_dev.argtypes = [vp, C.POINTER(MoeLayer), vp, i32, vp, vp, vp, vp]
+        L.rbt_hip_moe_dev_noalloc.argtypes = [vp, C.POINTER(MoeLayer), vp, i32, vp, vp, vp, vp]
         L.rbt_hip_reserve.argtypes = [vp, C.POINTER(MoeLayer), i32]
         L.rbt_hip_expert_counts_dev.argtypes, L.rbt_hip_expert_counts_dev.restype = [vp], vp
         L.rbt_hip_matvec.argtypes = [vp, vp, u64, vp, i32, i32]
@@ -333,6 +335,11 @@ class Device:
         vp = lambda b: None if b is None else (b if isinstance(b, C.c_void_p) else b.p)
         self._check(self.L.rbt_hip_moe_dev(self.h, C.byref(layer), vp(xb), T, vp(x), vp(moe), vp(routing),
                                            vp(weights)))
+
+    def moe_dev_noalloc(self, layer, xb, T, x=None, moe=None, routing=None, weights=None):
+        vp = lambda b: None if b is None else (b if isinstance(b, C.c_void_p) else b.p)
+        self._check(self.L.rbt_hip_moe_dev_noalloc(self.h, C.byref(layer), vp(xb), T, vp(x), vp(moe), vp(routing),
+                                                   vp(weights)))
 
     def reserve(self, layer, max_tokens):
         self._check(self.L.rbt_hip_reserve(self.h, C.byref(layer), max_tokens))
