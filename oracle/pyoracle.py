@@ -11,7 +11,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# RBT_ORACLE_LIB: another build of the same source (the sanitizer test loads an instrumented one)
+LIB_PATH = os.environ.get("RBT_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_BIN = os.path.join(HERE, "_ref", "rabbit2")
 
 DT_F32, DT_BF16 = 0, 1

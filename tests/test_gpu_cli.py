@@ -171,3 +171,43 @@ def test_generate_stream_reports_ids_in_order(dev):
     assert seen == want[:5] and out == want[:5]
     ids, _ = dev.generate(fx["tokens"], spec["n_gen"])  # the plain loop after a stopped stream
     assert ids == want
+
+
+PATCHED = os.path.join(ROOT, "oracle", "_ref", "rabbit2_hip")
+
+
+def host_has_avx2():
+    try:
+        return any("avx2" in ln.split() for ln in open("/proc/cpuinfo") if ln.startswith("flags"))
+    except OSError:
+        return False
+
+
+@pytest.mark.skipif(not os.path.exists(PATCHED), reason="patched reference engine not built (oracle/Makefile ref_hip)")
+@pytest.mark.parametrize("case", ["tiny_olmoe_bf16", "ref_bf16", "ref_odd_shape", "olmoe_layer_bf16"])
+def test_reference_engine_with_the_hip_seam(tmp_path, case):
+    """The reference engine itself with the integration patch (rabbitm2_amd/host/rabbit2_hip.patch):
+    --kernel hip sends every layer's MoE block to rbt_hip_moe (host pointers) while attention, the dense
+    matvecs and sampling stay on the CPU in the engine's own code. Against the reference's fixtures in the
+    order --kernel hip picks on this host (auto): routing identical, logits normwise within 1e-3, --gen
+    ids identical."""
+    spec, cfg, path = write_case(case, tmp_path)
+    fx = np.load(os.path.join(GOLDEN, case + ".npz"))
+    tag = "avx2" if host_has_avx2() else "scalar"
+    tokens = [str(int(t)) for t in fx["tokens"]]
+    lp, rp = tmp_path / "logits.bin", tmp_path / "routing.bin"
+    print(f"rabbit2_hip {case} --dump --kernel hip", flush=True)
+    res = subprocess.run([PATCHED, str(path), "--dump", str(lp), str(rp), "--kernel", "hip"] + tokens,
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr
+    assert "matvec kernel: hip-gfx950" in res.stderr
+    routing = np.fromfile(rp, dtype="<i4").reshape(len(tokens), cfg.n_layers, cfg.top_k)
+    logits = np.fromfile(lp, dtype="<f4").reshape(len(tokens), cfg.vocab)
+    assert np.array_equal(routing, fx[f"routing_{tag}"])
+    worst = max(normwise_err(logits[p], fx[f"logits_{tag}"][p]) for p in range(len(tokens)))
+    assert worst <= LOGIT_RTOL, worst
+    res = subprocess.run([PATCHED, str(path), "--gen", str(spec["n_gen"]), "--kernel", "hip"] + tokens,
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr
+    assert [int(t) for t in res.stdout.split()] == fx[f"gen_{tag}"].tolist()
+    print(f"{case}: routing identical, worst logits error {worst:.2e}", flush=True)
