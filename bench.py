@@ -544,6 +544,7 @@ def profile_prefill(calls):
     moe = dev.malloc(T * D * 4)
     bias_dev = dev.upload_array(np.array([2.0] * 8 + [0.0] * (E - 8), np.float32))
     dev.set_router_order(rh.ORDER_AVX2)
+    dev.prefill_layout(rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride))
     t0 = time.perf_counter()
     for bias in (None, bias_dev):
         L = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride, bias)
@@ -654,6 +655,9 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
     alg_bytes = E * 3 * H * D * esz + E * D * esz + T * D * 2 + T * D * 4
     alg_flops = T * 2 * E * D + P * 6 * H * D
     gemm_flops = {"gateup": P * 4 * H * D, "down_combine": P * 2 * H * D}
+    # the grouped GEMMs read the tiled copy of the experts made here where they take 128-row tiles
+    layer0 = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride)
+    dev.prefill_layout(layer0)
     res = {}
     for name, bias in (("uniform", None), ("skewed", bias_dev)):
         L = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride, bias)  # layer 0
@@ -702,7 +706,11 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
                 kern[kname] = {"avg_us": round(1000.0 * tot / n, 2)}
         dev.profile(0)
         counts = dev.expert_counts(E)
-        tiles = int(sum((c + 63) // 64 for c in counts))  # the GEMMs' 64-row tiles
+        # the GEMMs' row tiles, by the device's rule: 32 rows while the experts average at most 16, else
+        # 128 rows where 1.4 x their count is below the count of 64-row tiles, else 64
+        n64, n128 = (int(sum((c + m - 1) // m for c in counts)) for m in (64, 128))
+        tile_rows = 32 if P <= 16 * E else (128 if 7 * n128 < 5 * n64 else 64)
+        tiles = int(sum((c + tile_rows - 1) // tile_rows for c in counts))
         issued_rows = int(sum((c + 15) // 16 * 16 for c in counts))
         for kname, fl in gemm_flops.items():
             if kname in kern:
@@ -723,9 +731,12 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             "mfma_util_alg": round(alg_flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             "kernels": kern,
             "tokens_per_expert": [int(c) for c in counts],
+            "tile_rows": tile_rows,
             "row_tiles": tiles,
         }
+    dev.prefill_layout_drop(layer0)
     out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,
+           "expert_layout": "128-row tiles read the tiled copy (rbt_hip_prefill_layout), 64-row tiles the blobs",
            "note": f"per-call time of the whole MoE block (router .. combine), HIP graph of {PREFILL_GRAPH_CALLS} "
                    "calls replayed (us_per_call_eager: back-to-back eager calls), inputs in HBM",
            **res}

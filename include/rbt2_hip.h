@@ -83,7 +83,14 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *                         weights: (token, slot) pairs dispatched into per-expert lists and the
  *                         expert FFN run as grouped GEMMs on the matrix cores, each expert's weights
  *                         read once per call. Smaller T runs one GEMV per pair. Routing is the same
- *                         either way; outputs agree within the parity tolerance. */
+ *                         either way; outputs agree within the parity tolerance.
+ *   "prefill_layout"      1 (default): the grouped GEMMs read the tiled expert copies made by
+ *                         rbt_hip_prefill_layout, and rbt_hip_upload* makes them; 0: the blobs only.
+ *   "prefill_tile_rows"   0 (default): the grouped GEMMs take tiles of 32 rows of an expert's list
+ *                         while the experts average at most 16 rows, else 64 or 128 rows as the
+ *                         device picks from the call's tokens-per-expert histogram; 32 / 64 / 128:
+ *                         that tile height always (128 where the shape has it). Outputs agree within
+ *                         the parity tolerance (the reduction runs in other chunks). */
 int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
 
 /* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the
@@ -109,6 +116,18 @@ int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]);
 int rbt_hip_expert_stats(rbt_hip *h, uint64_t stats[6]);
 /* Device view of layer `layer` of the uploaded model (for the _dev calls). */
 int rbt_hip_layer(rbt_hip *h, int layer, rbt_moe_layer *out);
+/* The grouped (prefill) path's HBM layout (no counterpart in the reference: an optimisation of the
+ * device copy). The 128-row grouped GEMMs stream a layer's experts tile by tile; in the engine's
+ * row-major blobs each step of a tile spans 256 rows 4 KiB apart, which HBM serves at ~5 TB/s.
+ * rbt_hip_prefill_layout keeps a second copy of layer L's experts (the same 3 * H * D bf16 per expert)
+ * in tile order, each step contiguous (~7 TB/s); L NULL: every layer of the loaded model, which
+ * rbt_hip_upload / rbt_hip_upload_file build by themselves while the device has room (option
+ * "prefill_layout"). bf16 experts, dim a multiple of 256, expert_hidden of 256. The copy is taken
+ * from the blobs now, on the handle stream: after they change, call it again. Keyed by L->experts;
+ * dropped with the model, by rbt_hip_prefill_layout_drop (L NULL: all) or rbt_hip_free. Outputs are
+ * bit for bit the same with or without it. */
+int rbt_hip_prefill_layout(rbt_hip *h, const rbt_moe_layer *L);
+int rbt_hip_prefill_layout_drop(rbt_hip *h, const rbt_moe_layer *L);
 
 /* ---- the MoE block (replaces rabbit2.c:513-542; the rmsnorm at :512 stays with the caller) ----
  * xb [T][dim] normalised input. x_inout [T][dim] receives x += moe (may be NULL).

@@ -91,6 +91,14 @@ struct DecodeState {
     StepState *st = nullptr;      // [n_seq]
 };
 
+// A tiled copy of one layer's experts (launch_prefill_layout), taken from the blobs at `experts`.
+struct TiledLayer {
+    const void *experts = nullptr;
+    uint64_t stride = 0;
+    int E = 0, D = 0, H = 0;
+    void *buf = nullptr;
+};
+
 struct Workspace {
     int tokens = 0, E = 0, K = 0, H = 0;
     float *probs = nullptr;       // [T][E]
@@ -123,6 +131,7 @@ struct rbt_hip {
     Sampling sampling;     // rbt_hip_set_sampling: how rbt_hip_generate* pick tokens
     uint64_t seed = 0;
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
+    int prefill_tile_rows = 0;  // option "prefill_tile_rows": rows per grouped-GEMM tile, 0 = by batch
     const int32_t *expert_counts = nullptr;  // histogram of the last grouped-path call
     // staging for the host-pointer entry points: device buffer and its pinned host twin
     void *stage = nullptr;
@@ -138,6 +147,10 @@ struct rbt_hip {
     int tok_host_n = 0;
     // this device's scratch array (rbt_hip_moe_dev_noalloc), from hipGetSymbolAddress at init
     void *scratch = nullptr;
+    // tiled copies of layers' experts for the 128-row grouped GEMMs (rbt_hip_prefill_layout), keyed by
+    // the layer's expert blobs; option "prefill_layout" (default 1) uses them and builds them at upload
+    std::vector<TiledLayer> tiled;
+    int prefill_layout = 1;
     // expert residency counters in the engine's cache-stats terms (rabbit2.c:745-751): every expert is
     // read from the file once at upload (a miss) and every later use of a selected expert is a hit
     uint64_t cache_hits = 0, cache_misses = 0;
@@ -462,6 +475,70 @@ int parse_header(ModelLayout *m, const unsigned char *d, uint64_t file_size, rbt
     return 1;
 }
 
+// The tiled copy registered for layer L's experts, or nullptr (none, option off, other shape).
+const void *tiled_for(const rbt_hip *h, const rbt_moe_layer *L) {
+    if (!h->prefill_layout || L->dtype != RBT_DT_BF16) return nullptr;
+    for (const TiledLayer &t : h->tiled)
+        if (t.experts == L->experts && t.stride == L->expert_stride && t.E == L->n_experts && t.D == L->dim &&
+            t.H == L->expert_hidden)
+            return t.buf;
+    return nullptr;
+}
+
+// Frees the tiled copies whose blobs lie in [lo, hi) (all of them for lo = hi = nullptr). The stream
+// is idle: callers synchronise first.
+void tiled_drop(rbt_hip *h, const uint8_t *lo, const uint8_t *hi) {
+    std::vector<TiledLayer> keep;
+    for (TiledLayer &t : h->tiled) {
+        const uint8_t *p = static_cast<const uint8_t *>(t.experts);
+        if (lo == nullptr || (p >= lo && p < hi))
+            (void)hipFree(t.buf);
+        else
+            keep.push_back(t);
+    }
+    h->tiled.swap(keep);
+}
+
+// Builds (or rebuilds in place) the tiled copy of layer L's experts, asynchronously on the handle stream.
+int tiled_build(rbt_hip *h, const rbt_moe_layer *L) {
+    if (L->dtype != RBT_DT_BF16 || !prefill_layout_supported(L->dtype, L->dim, L->expert_hidden))
+        return fail(h, "prefill_layout: no tiled layout for dtype %d, dim %d, expert_hidden %d (bf16, dim a "
+                       "multiple of 256 and expert_hidden of 256)", L->dtype, L->dim, L->expert_hidden);
+    if (!L->experts || L->n_experts < 1 || L->expert_stride % 16 != 0 ||
+        (reinterpret_cast<uintptr_t>(L->experts) & 15u))
+        return fail(h, "prefill_layout: bad layer (experts NULL or not 16-byte aligned)");
+    TiledLayer *t = nullptr;
+    for (TiledLayer &x : h->tiled)
+        if (x.experts == L->experts) t = &x;
+    if (t && (t->stride != L->expert_stride || t->E != L->n_experts || t->D != L->dim || t->H != L->expert_hidden)) {
+        HIP_OK(h, hipStreamSynchronize(h->stream));
+        (void)hipFree(t->buf);
+        t->buf = nullptr;
+    }
+    if (!t) {
+        h->tiled.push_back(TiledLayer{});
+        t = &h->tiled.back();
+        t->experts = L->experts;
+    }
+    t->stride = L->expert_stride;
+    t->E = L->n_experts;
+    t->D = L->dim;
+    t->H = L->expert_hidden;
+    if (!t->buf) {
+        const hipError_t e = HIP_TRY(hipMalloc(&t->buf, prefill_layout_bytes(t->E, t->D, t->H)));
+        if (e != hipSuccess) {
+            h->tiled.erase(h->tiled.begin() + (t - h->tiled.data()));  // keep no entry without a copy
+            return fail(h, "prefill_layout: hipMalloc of %llu bytes failed: %s",
+                        (unsigned long long)prefill_layout_bytes(L->n_experts, L->dim, L->expert_hidden),
+                        hipGetErrorString(e));
+        }
+    }
+    Launch Lx;
+    Lx.s = h->stream;
+    HIP_OK(h, launch_prefill_layout(Lx, L->experts, L->expert_stride, L->n_experts, L->dim, L->expert_hidden, t->buf));
+    return 1;
+}
+
 // Drops the handle's model image and decode state (the workspace stays: it depends on shapes only).
 // Afterwards the handle holds no model until a new layout is adopted with its image.
 int model_drop(rbt_hip *h) {
@@ -471,7 +548,10 @@ int model_drop(rbt_hip *h) {
     h->ds = DecodeState{};
     (void)hipFree(h->rhist);
     h->rhist = nullptr;
-    if (h->model) (void)hipFree(h->model);
+    if (h->model) {
+        tiled_drop(h, h->model, h->model + h->model_size);
+        (void)hipFree(h->model);
+    }
     h->model = nullptr;
     h->model_size = 0;
     h->cfg = rbt_config{};
@@ -518,7 +598,7 @@ int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float 
     HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown),
                              next_nw ? no_combine : lc(h, kProfCombine), L->experts, L->expert_stride, xb, T,
                              L->n_experts, L->top_k, L->dim, L->expert_hidden, routing, w.weights, w.hbuf, w.pre, x,
-                             nullptr, &counts, true, next_nw == nullptr));
+                             nullptr, &counts, true, next_nw == nullptr, h->prefill_tile_rows, tiled_for(h, L)));
     h->expert_counts = counts;
     if (next_nw) {  // the combine, fused with the RMSNorm the next step starts with (xb and its planes)
         const float *y = nullptr;
@@ -816,7 +896,8 @@ int moe_block(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, fl
         int32_t *counts = nullptr;
         HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
                                  L->experts, L->expert_stride, xb_dev, T, L->n_experts, L->top_k, L->dim,
-                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts, fused));
+                                 L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts, fused,
+                                 true, h->prefill_tile_rows, tiled_for(h, L)));
         h->expert_counts = counts;
         return done();
     }
@@ -891,6 +972,7 @@ void rbt_hip_free(rbt_hip *h) {
     if (h->pin) (void)hipHostFree(h->pin);
     (void)hipFree(h->rhist);
     if (h->tok_host) (void)hipHostFree(h->tok_host);
+    tiled_drop(h, nullptr, nullptr);
     (void)hipFree(h->model);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
@@ -902,6 +984,33 @@ int rbt_hip_set_router_order(rbt_hip *h, int order) {
     if (!h) return fail(nullptr, "set_router_order: handle is NULL");
     if (order != RBT_ORDER_SCALAR && order != RBT_ORDER_AVX2) return fail(h, "router order must be 0 or 1");
     h->order = order;
+    return 1;
+}
+
+// The tiled copies of every layer of the uploaded model. at_upload: only with option "prefill_layout"
+// on, for a shape that has one and while the device keeps 1 GiB free besides; nothing built is no
+// error there (the grouped GEMMs then read the blobs).
+int tiled_build_model(rbt_hip *h, bool at_upload) {
+    const rbt_config &c = h->cfg;
+    if (at_upload) {
+        if (!h->prefill_layout || c.dtype != RBT_DT_BF16 || !prefill_layout_supported(c.dtype, c.dim, c.expert_hidden))
+            return 1;
+        size_t free_b = 0, total_b = 0;
+        if (hipMemGetInfo(&free_b, &total_b) != hipSuccess ||
+            free_b < (size_t)c.n_layers * prefill_layout_bytes(c.n_experts, c.dim, c.expert_hidden) + (1ull << 30))
+            return 1;
+    }
+    for (int l = 0; l < c.n_layers; l++) {
+        rbt_moe_layer ml;
+        if (!rbt_hip_layer(h, l, &ml) || !tiled_build(h, &ml)) {
+            if (!at_upload) return 0;
+            // at upload the copies are an optimisation: without them the model is complete
+            (void)hipStreamSynchronize(h->stream);
+            tiled_drop(h, h->model, h->model + h->model_size);
+            h->err[0] = '\0';
+            return 1;
+        }
+    }
     return 1;
 }
 
@@ -920,7 +1029,7 @@ int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config 
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
-    return 1;
+    return tiled_build_model(h, true);
 }
 
 int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
@@ -962,7 +1071,7 @@ int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
-    return 1;
+    return tiled_build_model(h, true);
 }
 
 int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]) {
@@ -1004,6 +1113,27 @@ int rbt_hip_expert_stats(rbt_hip *h, uint64_t stats[6]) {
     stats[3] = h->cache_misses * h->expert_stride;  // bytes_read == misses * expert_stride
     stats[4] = all * h->expert_stride;             // resident_bytes
     stats[5] = all * h->expert_stride;             // capacity_bytes
+    return 1;
+}
+
+int rbt_hip_prefill_layout(rbt_hip *h, const rbt_moe_layer *L) {
+    if (!h) return fail(nullptr, "prefill_layout: handle is NULL");
+    if (!set_device(h)) return 0;
+    if (L) return tiled_build(h, L);
+    if (!h->model) return fail(h, "prefill_layout: no model (pass a layer, or upload a model first)");
+    return tiled_build_model(h, false);
+}
+
+int rbt_hip_prefill_layout_drop(rbt_hip *h, const rbt_moe_layer *L) {
+    if (!h) return fail(nullptr, "prefill_layout_drop: handle is NULL");
+    if (!set_device(h)) return 0;
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    if (!L) {
+        tiled_drop(h, nullptr, nullptr);
+        return 1;
+    }
+    const uint8_t *p = static_cast<const uint8_t *>(L->experts);
+    tiled_drop(h, p, p + 1);
     return 1;
 }
 
@@ -1251,6 +1381,8 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
         h->fused_decode = value != 0;
     } else if (strcmp(name, "batch_mfma") == 0) {
         h->batch_mfma = value != 0;
+    } else if (strcmp(name, "prefill_layout") == 0) {
+        h->prefill_layout = value != 0;
     } else if (strcmp(name, "attn_last_merge") == 0) {
         h->attn_last_merge = value != 0;
     } else if (strcmp(name, "routing_history") == 0) {
@@ -1258,6 +1390,10 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
     } else if (strcmp(name, "prefill_min_tokens") == 0) {
         if (value < 1 || value > 65536) return fail(h, "set_option: prefill_min_tokens must be in [1, 65536]");
         h->prefill_min_tokens = (int)value;
+    } else if (strcmp(name, "prefill_tile_rows") == 0) {
+        if (value != 0 && value != 32 && value != 64 && value != 128)
+            return fail(h, "set_option: prefill_tile_rows must be 0, 32, 64 or 128");
+        h->prefill_tile_rows = (int)value;
     } else {
         return fail(h, "set_option: unknown option '%s'", name);
     }

@@ -16,10 +16,10 @@
 //    instead of 8. A full 64-row tile then does 64 rows x 2 parts x 2 flop = 256 flop per weight
 //    element, 128 flop per weight byte: below the bf16 MFMA/HBM ridge (2.5 PFLOP/s / 8 TB/s =
 //    312), so the kernels stay bound by HBM.
-//    Tiles: 64 rows x 256 weight rows per block of 16 waves (or 32 x 128 per 8 waves for decode-sized
-//    batches);
-//    the reduction runs in chunks of 64 (128) through a three-stage LDS ring filled by direct
-//    HBM -> LDS copies (weights and activations).
+//    Tiles: 128 or 64 rows x 256 weight rows per block of 16 waves (or 32 x 128 per 8 waves for
+//    decode-sized batches); the reduction runs in chunks of 32, 64 (128) through a four- or three-stage
+//    LDS ring filled by direct HBM -> LDS copies (weights and activations). 128-row tiles cover the
+//    whole list of an expert with up to 128 rows, so its weight tile is streamed by one block once.
 //    Tile order (expert, column tile, row tile), split into 8 contiguous ranges, one per XCD (the
 //    hardware hands block b to XCD b % 8): the row tiles of a hot expert then share each weight
 //    tile in that XCD's L2, and an expert's activation rows are reused across its column tiles.
@@ -27,6 +27,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "rbt2_internal.h"
 
@@ -41,7 +42,11 @@ constexpr int kDispatchMaxE = 256;
 // ---------------------------------------------------------------- dispatch (one block, 1024 threads)
 // routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);
 // perm[P]: pair ids grouped by expert, increasing within an expert; pos_of[P]: inverse of perm;
-// m_off[E+1]: exclusive prefix of ceil(counts / mt_rows) (the grouped GEMMs' row tiles per expert).
+// m_off[E+1]: exclusive prefix of ceil(counts / mt_rows) (the grouped GEMMs' row tiles per expert);
+// with m_off2 given, also m_off2[E+1] for 128-row tiles and *choice, the tile height the grouped GEMMs
+// take (1: 128 rows, 0: mt_rows): tall = 2 forces 128, 1 forces mt_rows, 0 picks 128 when
+// 1.4 x its tile count is below the mt_rows tile count (a 128-row tile takes ~1.4x as long as a 64-row
+// one, measured on the OLMoE layer at 512 tokens with uniform and skewed routing).
 // Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
 // equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
 // row; a pair's rank inside its wave's slice goes to pos_of as a temporary. B: wave 0 (4 experts per
@@ -50,7 +55,9 @@ constexpr int kDispatchMaxE = 256;
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ routing, int P, int E,
                                                         int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ perm, int32_t *__restrict__ pos_of,
-                                                        int32_t *__restrict__ m_off, int mt_rows) {
+                                                        int32_t *__restrict__ m_off, int mt_rows,
+                                                        int32_t *__restrict__ m_off2, int32_t *__restrict__ choice,
+                                                        int tall) {
     constexpr int NW = 16;
     __shared__ int s_w[NW][kDispatchMaxE];  // A: running counts per wave; B: each wave's base positions
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -77,7 +84,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
     }
     __syncthreads();
     if (wv == 0) {
-        int c[4], mt[4];
+        int c[4], mt[4], mt2[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = 4 * lane + i;
@@ -86,19 +93,22 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                 for (int w = 0; w < NW; ++w) tot += s_w[w][e];
             c[i] = tot;
             mt[i] = (tot + mt_rows - 1) / mt_rows;
+            mt2[i] = (tot + 127) / 128;
         }
         // exclusive scans across the wave of the lanes' sums (4 experts per lane, ascending)
         int sc = ((c[0] + c[1]) + c[2]) + c[3], sm = ((mt[0] + mt[1]) + mt[2]) + mt[3];
-        int ic = sc, im = sm;
+        int sm2 = ((mt2[0] + mt2[1]) + mt2[2]) + mt2[3];
+        int ic = sc, im = sm, im2 = sm2;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
-            const int uc = __shfl_up(ic, d, 64), um = __shfl_up(im, d, 64);
+            const int uc = __shfl_up(ic, d, 64), um = __shfl_up(im, d, 64), um2 = __shfl_up(im2, d, 64);
             if (lane >= d) {
                 ic += uc;
                 im += um;
+                im2 += um2;
             }
         }
-        int oc = ic - sc, om = im - sm;
+        int oc = ic - sc, om = im - sm, om2 = im2 - sm2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = 4 * lane + i;
@@ -106,6 +116,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                 counts[e] = c[i];
                 offsets[e] = oc;
                 m_off[e] = om;
+                if (m_off2) m_off2[e] = om2;
                 int run = oc;  // each wave's first position for expert e
                 for (int w = 0; w < NW; ++w) {
                     const int n = s_w[w][e];
@@ -116,9 +127,15 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
             if (e == E - 1) {
                 offsets[E] = oc + c[i];
                 m_off[E] = om + mt[i];
+                if (m_off2) {
+                    m_off2[E] = om2 + mt2[i];
+                    const int n64 = om + mt[i], n128 = om2 + mt2[i];
+                    *choice = tall == 2 ? 1 : (tall == 1 ? 0 : (int)(7 * n128 < 5 * n64));
+                }
             }
             oc += c[i];
             om += mt[i];
+            om2 += mt2[i];
         }
     }
     __syncthreads();
@@ -167,12 +184,33 @@ template <int N>
 __device__ __forceinline__ void wait_dma() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Until at most `ahead` stages of n copies each (n = WI .. WI + AI, this wave's copies per stage) are
+// outstanding; copies complete in issue order. Both arguments are wave-uniform.
+template <int WI, int AI>
+__device__ __forceinline__ void wait_stages(int ahead, int n) {
+    static_assert(AI <= 2, "copies per stage");
+    if (ahead <= 0) {
+        wait_dma<0>();
+    } else if (ahead == 1) {
+        if (n == WI) wait_dma<WI>();
+        else if (n == WI + 1) wait_dma<WI + 1>();
+        else wait_dma<WI + 2>();
+    } else {
+        if (n == WI) wait_dma<2 * WI>();
+        else if (n == WI + 1) wait_dma<2 * (WI + 1)>();
+        else wait_dma<2 * (WI + 2)>();
+    }
+}
 
 // Tile: ROWS list rows x WROWS weight rows (gate/up: half W1 rows, the same rows of W3; down: W2
-// rows), the reduction in chunks that are one ring stage in LDS each; three stages, the copies of
-// stages c+1 and c+2 in flight while the MFMAs run on stage c:
-//   ROWS = 64: 256 weight rows x 128 B (k-chunks of 64) + 2 x 64 activation rows x 128 B = 48 KiB
-//   ROWS = 32: 128 weight rows x 256 B (k-chunks of 128) + 2 x 32 activation rows x 256 B = 48 KiB
+// rows), the reduction in chunks that are one ring stage in LDS each; three (four) stages, the copies
+// of the next two (three) stages in flight while the MFMAs run on the current one:
+//   64 x 256:  256 weight rows x 128 B (k-chunks of 64) + 2 x 64 activation rows x 128 B = 48 KiB
+//   32 x 128:  128 weight rows x 256 B (k-chunks of 128) + 2 x 32 activation rows x 256 B = 48 KiB
+// A block's throughput is set by the copies it keeps in flight (two stages, ~96 KiB, about 33 GB/s per
+// CU whatever the source, weights from HBM or activation rows from L2), so activation copies of row
+// groups past the end of the list are not issued (their LDS rows hold stale data, which only reaches
+// output rows that are never written).
 // (the activation rows: bf16 hi and lo planes). The kernel is bound by its copies: it keeps 90% of
 // its time with the MFMAs and operand reads taken out, and a stage takes ~1.45 us whether two or
 // three stages are in flight and whether a row is read in 128- or 256-byte runs. At 5.8 TB/s of
@@ -182,9 +220,9 @@ __device__ __forceinline__ void wait_dma() {
 // per wave.
 constexpr int kGWRows = 256, kGKC = 64;  // the 64-row tile; prefill_supported's shape rules
 constexpr int kSmallTileRowsPerExpert = 16;  // mean list rows per expert up to which tiles have 32 rows
-template <int ROWS>
+template <int ROWS, int WROWS>
 struct GTile {
-    static constexpr int kWRows = ROWS == 64 ? 256 : 128;  // weight rows per tile
+    static constexpr int kWRows = WROWS;                   // weight rows per tile
     static constexpr int kKC = ROWS == 64 ? 64 : 128;      // k per stage
     static constexpr int kRowB = 2 * kKC;                  // bytes of each row per stage
     static constexpr int kGran = kRowB / 16;               // 16-byte granules per row per stage
@@ -193,20 +231,22 @@ struct GTile {
     static constexpr int kWBytes = kWRows * kRowB;         // 32 KiB
     static constexpr int kABytes = ROWS * kRowB;
     static constexpr int kStageBytes = kWBytes + 2 * kABytes;
-    static constexpr int kWaves = ROWS == 64 ? 16 : 8;    // waves per block (each needs a W1/W3 pair)
+    static constexpr int kWaves = ROWS == 32 ? 8 : 16;    // waves per block (each needs a W1/W3 pair)
     static constexpr int kRG = ROWS / 16;                  // row groups of 16 (one per wave)
     static constexpr int kCH = kWaves / kRG;               // weight-row splits (waves per row group)
     static constexpr int kNB = kWRows / 16 / kCH;          // weight blocks of 16 per wave
     static constexpr int kWI = kWBytes / 1024 / kWaves;    // weight copies per wave per stage
     static constexpr int kACP = kABytes / 1024;            // copies per activation plane
     static constexpr int kAI = 2 * kACP / kWaves;          // activation copies per wave per stage
-    static constexpr int kDmaPerWave = kWI + kAI;
-    static_assert((ROWS == 64 || ROWS == 32) && kStages * kStageBytes <= 160 * 1024 &&
+    static constexpr int kDmaPerWave = kWI + kAI;  // at most: activation copies past the list are skipped
+    static_assert(((ROWS == 64 && WROWS == 256) || (ROWS == 32 && WROWS == 128)) &&
+                      kStages * kStageBytes <= 160 * 1024 &&
                       kAI * kWaves == 2 * kACP && kWI * kWaves * 1024 == kWBytes && kNB >= 2 && kNB % 2 == 0,
                   "tile shape");
-    // Inside a stage, row r's granule g sits at slot swz(r, g): the MFMA operand reads (16 consecutive
-    // rows at one granule per 16 lanes) then hit 16 distinct bank groups (two rows per 256 bytes of
-    // banks for 128-byte rows, one for 256-byte rows).
+    // Inside a stage, row r's granule g sits at slot swz(r, g) (an involution in g, so the copies can
+    // place it by choosing their source granule): the MFMA operand reads (16 consecutive rows at one
+    // granule per 16 lanes) then hit 16 distinct bank groups (two rows per 256 bytes of banks for
+    // 128-byte rows, one for 256-byte rows).
     __device__ static int swz(int r, int g) { return kRowB == 128 ? g ^ ((r >> 1) & 7) : g ^ (r & 15); }
 };
 
@@ -217,18 +257,19 @@ struct GTile {
 // rows (kNB blocks of 16: gate/up W1 blocks (kNB/2) ch .. and the matching W3 blocks; down W2 blocks
 // kNB ch ..).
 // Requirements (prefill_supported): N % (256 / MATS) == 0, Kd % 64 == 0, 16-byte aligned rows.
-template <int MATS, int ROWS>
-__global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kernel(
-    const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
-    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
-    int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+// The block's work on tile slot `bid` (the kernels below pass blockIdx.x); ring: the LDS ring of
+// STAGES * SBYTES bytes at LDS offset ring0.
+template <int MATS, int ROWS, int WROWS>
+__device__ __forceinline__ void gemm_lds_tile(
+    uint8_t *ring, uint32_t ring0, unsigned bid, const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off,
+    uint64_t w3_off, int N, int Kd, const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather,
+    const int32_t *__restrict__ perm, int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
     uint16_t *__restrict__ out_lo) {
-    using TS = GTile<ROWS>;
-    constexpr int WROWS = TS::kWRows, NTILE = WROWS / MATS;  // output columns per tile
+    using TS = GTile<ROWS, WROWS>;
+    constexpr int NTILE = WROWS / MATS;  // output columns per tile
     constexpr int STAGES = TS::kStages, SBYTES = TS::kStageBytes, NB = TS::kNB, AI = TS::kAI, WI = TS::kWI;
     constexpr int ROWB = TS::kRowB, GRAN = TS::kGran, RPC = TS::kRowsPerCopy, WBYTES = TS::kWBytes;
-    __shared__ __align__(1024) uint8_t ring[STAGES * SBYTES];
 
     // w in a scalar register: the branches on it below are then wave-uniform jumps, not exec masks
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), rg = w % TS::kRG,
@@ -236,8 +277,8 @@ __global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kern
     const int ntiles_n = N / NTILE;
     const int total = m_off[E] * ntiles_n;
     const int range = (total + 7) >> 3;
-    const int slot = (int)(blockIdx.x >> 3);
-    const int tau = (int)(blockIdx.x & 7) * range + slot;
+    const int slot = (int)(bid >> 3);
+    const int tau = (int)(bid & 7) * range + slot;
     if (slot >= range || tau >= total) return;
     int lo = 0, hi = E - 1;  // the expert owning tile tau: the last e with m_off[e] * ntiles_n <= tau
     while (lo < hi) {
@@ -252,7 +293,7 @@ __global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kern
     const int local = tau - m_off[e] * ntiles_n;
     const int jt = local / me, il = local - jt * me;
     const int row0 = offsets[e] + il * ROWS;
-    const int rows = min(ROWS, counts[e] - il * ROWS);
+    const int rows = __builtin_amdgcn_readfirstlane(min(ROWS, counts[e] - il * ROWS));  // uniform: scalar branches below
     const int n0 = jt * NTILE;
     const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
 
@@ -272,16 +313,19 @@ __global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kern
         wsrc[i] = base + (size_t)wr * rowb + 16 * g;
     }
     const uint8_t *asrc[AI];
+    bool aon[AI];  // wave-uniform: the copy covers at least one row of the list
+    int ncopy = WI;  // copies this wave issues per stage
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
         // copy u: plane u / kACP, rows RPC * (u % kACP) ..
         const int u = AI * w + i, plane = u / TS::kACP, r = RPC * (u % TS::kACP) + lane / GRAN,
                   g = TS::swz(r, lane % GRAN);
-        const int lr = row0 + (r < rows ? r : 0);  // rows past the list re-read its first row
+        aon[i] = RPC * (u % TS::kACP) < rows;
+        ncopy += aon[i] ? 1 : 0;
+        const int lr = row0 + (r < rows ? r : 0);  // rows past the list (in a copy that is issued) re-read its first row
         const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
         asrc[i] = reinterpret_cast<const uint8_t *>(plane ? a_lo : a_hi) + arow * rowb + 16 * g;
     }
-    const uint32_t ring0 = (uint32_t)(uintptr_t)ring;
     const int nch = Kd / TS::kKC;
     // Stage c reads k-chunk (c + rot) mod nch. Without the rotation every resident block streams the
     // same column window of its rows at the same time, so the whole chip's requests fall on the few
@@ -298,7 +342,7 @@ __global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kern
             lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (WI * w + i) * 1024));
 #pragma unroll
         for (int i = 0; i < AI; ++i)
-            lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + WBYTES + (AI * w + i) * 1024));
+            if (aon[i]) lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + WBYTES + (AI * w + i) * 1024));
     };
 
     // MFMA operand reads: lane -> row (lane % 16) of a 16-row block, logical granule 4*ks + lane / 16
@@ -323,12 +367,7 @@ __global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kern
     for (int c = 0; c < nch; ++c) {
         // stages c+1 .. c+STAGES-2 (as far as they exist) may still be in flight, stage c must have landed
         const int ahead = min(STAGES - 2, nch - 1 - c);
-        if (ahead >= 2)
-            wait_dma<2 * TS::kDmaPerWave>();
-        else if (ahead == 1)
-            wait_dma<TS::kDmaPerWave>();
-        else
-            wait_dma<0>();
+        wait_stages<WI, AI>(ahead, ncopy);
         __syncthreads();  // every wave's copies of stage c have landed
         if (c + STAGES - 1 < nch) issue(c + STAGES - 1);  // into the stage read at c-1: all waves are past it
         if (active) {
@@ -376,6 +415,301 @@ __global__ __launch_bounds__(64 * GTile<ROWS>::kWaves, 1) void grouped_gemm_kern
     }
 }
 
+template <int MATS, int ROWS, int WROWS>
+__global__ __launch_bounds__((64 * GTile<ROWS, WROWS>::kWaves), 1) void grouped_gemm_kernel(
+    const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
+    int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
+    uint16_t *__restrict__ out_lo) {
+    __shared__ __align__(1024) uint8_t ring[GTile<ROWS, WROWS>::kStages * GTile<ROWS, WROWS>::kStageBytes];
+    gemm_lds_tile<MATS, ROWS, WROWS>(ring, (uint32_t)(uintptr_t)ring, blockIdx.x, experts, stride, w_off, w3_off, N,
+                                     Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, out_f32, out_hi,
+                                     out_lo);
+}
+
+// ---------------------------------------------------------------- grouped GEMM, 128-row tiles
+// Where the dispatch kernel picks them, a tile holds up to 128 list rows and 256 weight rows
+// (gate/up: 128 W1 rows and the same 128 W3 rows; down: 256 W2 rows), one block of 16 waves per tile,
+// so a weight tile is streamed once for up to 128 rows. Wave W owns the 16 weight rows 16 W .. of the
+// tile (gate/up: W1 for W < 8, W3 for W >= 8; the two halves meet through LDS in the epilogue) and
+// loads their MFMA operands from HBM straight into registers three 64-wide k-steps ahead of its MFMAs;
+// the activation rows, which every wave multiplies, are loaded four k-steps ahead into registers and
+// pass through a two-stage LDS ring. The row groups past the end of the list are not multiplied.
+// Every wait is the compiler's own. Same operands, accumulation order and epilogue arithmetic as
+// grouped_gemm_kernel.
+constexpr int kWrRows = 128, kWrKC = 64, kWrAhead = 3, kWrWaves = 16;
+// buffer resources of the activation planes: records (bytes) past any valid offset, and the config
+// word of a raw 32-bit-format buffer
+constexpr int kWrBufRecords = 0x7FFF0000, kBufConfig = 0x00020000;
+// whole tiles of output columns, and k-steps a multiple of the kWrAhead + 1 register slots
+constexpr bool gemm_wr_supported(int mats, int N, int Kd) {
+    return N % (mats == 2 ? 128 : 256) == 0 && Kd % (kWrKC * (kWrAhead + 1)) == 0;
+}
+
+// The tiled copy of a layer's experts (prefill_layout_kernel): per expert (3 H D bf16, the size of its
+// blob) the gate/up part, then the down part, each [tile][k-chunk of 64][row block W 0..15][half s
+// 0..1][lane 0..63][16 bytes]: one tile's k-chunk is 32 KiB in the order gemm_wr_tile's
+// waves load it (1 KiB per load instruction), so each step of a tile reads contiguous memory (the
+// row-major blob spreads a step over 256 rows 4 KiB apart, which holds HBM to ~5 TB/s; contiguous
+// 32 KiB steps stream at ~6.9 TB/s). Lane l of block W holds tile row r = 16 W + (l & 15) at
+// k = 64 chunk + 32 s + 8 (l >> 4); gate/up tile jt: r < 128 -> W1 row 128 jt + r, else W3 row
+// 128 jt + r - 128; down tile jt: W2 row 256 jt + r.
+constexpr int kTiledChunk = 32768;
+__global__ __launch_bounds__(256) void prefill_layout_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
+                                                            int D, int H, uint8_t *__restrict__ dst,
+                                                            uint64_t units_per_expert) {
+    const uint64_t u = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int e = (int)blockIdx.y;
+    if (u >= units_per_expert) return;
+    const uint64_t gu_units = (uint64_t)H * D / 4;  // 16-byte units of the gate/up part (2 H D bf16)
+    const bool down = u >= gu_units;
+    const uint64_t v = down ? u - gu_units : u;
+    const int Kd = down ? H : D;
+    const uint64_t ch = v / (kTiledChunk / 16);
+    const int t = (int)(v % (kTiledChunk / 16)), W = t / 128, s = (t / 64) % 2, l = t % 64;
+    const int r = 16 * W + (l & 15);
+    const int nch = Kd / kWrKC;
+    const int jt = (int)(ch / nch), c = (int)(ch % nch);
+    const int k = kWrKC * c + 32 * s + 8 * (l >> 4);
+    const uint8_t *src = experts + (size_t)e * stride;
+    size_t off;
+    if (!down)
+        off = (r >= 128 ? (size_t)H * D * 2 : 0) + ((size_t)(128 * jt + (r & 127)) * D + k) * 2;
+    else
+        off = 2 * (size_t)H * D * 2 + ((size_t)(256 * jt + r) * H + k) * 2;
+    *reinterpret_cast<u32x4 *>(dst + (size_t)e * units_per_expert * 16 + u * 16) =
+        *reinterpret_cast<const u32x4 *>(src + off);
+}
+
+// The block's work on 128-row tile slot `bid`; smem: 2 * 2 * ABYTES bytes of LDS (the ring).
+template <int MATS>
+__device__ __forceinline__ void gemm_wr_tile(
+    uint8_t *smem, unsigned bid, const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
+    int N, int Kd, const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather,
+    const int32_t *__restrict__ perm, int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
+    uint16_t *__restrict__ out_lo, const uint8_t *__restrict__ tiled, uint64_t tiled_stride, uint64_t tiled_off) {
+    constexpr int NT = 64 * kWrWaves;             // threads
+    constexpr int NTILE = MATS == 2 ? 128 : 256;  // output columns per tile
+    constexpr int RG = kWrRows / 16;              // row groups of 16
+    constexpr int ROWB = 2 * kWrKC;               // bytes of an activation row per k-step
+    constexpr int ABYTES = kWrRows * ROWB;        // one plane of a k-step, 16 KiB
+    constexpr int AU = 2 * ABYTES / 16 / NT;      // 16-byte activation units per thread per k-step
+    constexpr int SLOTS = kWrAhead + 1;           // register sets of weights and of activations
+    static_assert(AU * NT * 16 == 2 * ABYTES && 2 * 2 * ABYTES >= (kWrWaves / 2) * RG * 64 * 16, "ring sizes");
+    uint8_t(*ring)[2 * ABYTES] = reinterpret_cast<uint8_t(*)[2 * ABYTES]>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, W = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ntiles_n = N / NTILE;
+    const int total = m_off[E] * ntiles_n;
+    const int range = (total + 7) >> 3;
+    const int slot = (int)(bid >> 3);
+    const int tau = (int)(bid & 7) * range + slot;
+    if (slot >= range || tau >= total) return;
+    int lo = 0, hi = E - 1;  // the expert owning tile tau: the last e with m_off[e] * ntiles_n <= tau
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (m_off[mid] * ntiles_n <= tau)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const int e = lo;
+    const int me = m_off[e + 1] - m_off[e];
+    const int local = tau - m_off[e] * ntiles_n;
+    const int jt = local / me, il = local - jt * me;
+    const int row0 = offsets[e] + il * kWrRows;
+    const int rows = __builtin_amdgcn_readfirstlane(min(kWrRows, counts[e] - il * kWrRows));
+    const int n0 = jt * NTILE;
+    const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
+    const int nch = Kd / kWrKC;
+    // Step c reads k-chunk (c + rot) mod nch, rot a function of the weight tile (see grouped_gemm_kernel)
+    const int rot = (e * ntiles_n + jt) % nch;
+    auto cidx = [&](int c) { return c + rot < nch ? c + rot : c + rot - nch; };
+
+    // weight operands of this lane: tile row 16 W + (lane & 15), k offset 8 * (lane >> 4) in each 32-wide
+    // half s of a 64-wide k-chunk cc, at wp + cc * wck + s * wsb (blobs: the row itself; tiled copy: the
+    // tile's contiguous 32 KiB chunks)
+    const uint8_t *wp;
+    size_t wck, wsb;
+    if (tiled) {
+        wp = tiled + (size_t)e * tiled_stride + tiled_off + (size_t)jt * nch * kTiledChunk + (size_t)(2 * W) * 1024 +
+             16 * lane;
+        wck = kTiledChunk;
+        wsb = 1024;
+    } else {
+        const int tr = 16 * W + (lane & 15);
+        const uint8_t *base = experts + (size_t)e * stride + (MATS == 2 && tr >= 128 ? w3_off : w_off);
+        const int wr = MATS == 2 ? n0 + (tr & 127) : n0 + tr;
+        wp = base + (size_t)wr * rowb + 16 * (lane >> 4);
+        wck = ROWB;
+        wsb = 64;
+    }
+    // activation units of this thread: u = tid + NT i -> plane i (u / (ABYTES / 16)), row, granule. They
+    // are buffer loads: a row past the end of the list gets an offset past the buffer's end, which returns
+    // zeros without a memory request (every request counts against the CU's in-flight limit, which the
+    // weight stream needs), and no branch (which keeps the compiler's waits exact). The buffers start at
+    // the tile's first row (list order) or the plane (gathered rows; the planes are below 2 GiB).
+    const size_t base_row = gather ? 0 : (size_t)row0;
+    const __amdgpu_buffer_rsrc_t rs[2] = {
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a_hi) + base_row * Kd, 0, kWrBufRecords, kBufConfig),
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a_lo) + base_row * Kd, 0, kWrBufRecords, kBufConfig)};
+    uint32_t aoff[AU], adst[AU];
+#pragma unroll
+    for (int i = 0; i < AU; ++i) {
+        const int u = tid + NT * i, r = (u % (ABYTES / 16)) / (ROWB / 16), g = u % (ROWB / 16);
+        static_assert(NT == ABYTES / 16, "one plane per unit index i");
+        const int lr = row0 + (r < rows ? r : 0);
+        const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
+        aoff[i] = r < rows ? (uint32_t)((arow - base_row) * rowb + 16 * g) : (uint32_t)kWrBufRecords;
+        adst[i] = (uint32_t)(i * ABYTES + r * ROWB + 16 * (g ^ ((r >> 1) & 7)));
+    }
+    // register sets: activations of k-step x in aset[x % SLOTS] (loaded four steps ahead, stored to the
+    // LDS ring one step ahead), weights of k-step x in wv[x % SLOTS] (loaded three steps ahead)
+    u32x4 aset[SLOTS][AU];
+    u32x4 wv[SLOTS][2];  // [slot][32-wide half]
+    auto load_a = [&](u32x4 (&dst)[AU], int c) {
+        const uint32_t kb = (uint32_t)(cidx(c) * ROWB);
+#pragma unroll
+        for (int i = 0; i < AU; ++i) dst[i] = __builtin_amdgcn_raw_buffer_load_b128(rs[i], (int)(aoff[i] + kb), 0, 0);
+    };
+    auto store_a = [&](const u32x4 (&src)[AU], int buf) {
+#pragma unroll
+        for (int i = 0; i < AU; ++i) *reinterpret_cast<u32x4 *>(&ring[buf][adst[i]]) = src[i];
+    };
+    auto load_w = [&](u32x4 (&dst)[2], int c) {
+        const size_t kb = (size_t)cidx(c) * wck;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) dst[s] = ld_stream_u4(wp + kb + s * wsb);
+    };
+
+    f32x4 acc[RG];
+#pragma unroll
+    for (int q = 0; q < RG; ++q) acc[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // k-step c on slot J = c % SLOTS; LAST: the tile's final SLOTS steps. nch is a multiple of SLOTS
+    // (gemm_wr_supported), so slots and the remaining loads are compile-time constants. Loads complete in
+    // issue order and a wait covers everything issued before its load, so each step stores the next
+    // step's activations, then issues activations before weights: the store at step c then waits for
+    // loads up to step c - 3's activations, never for weights still three steps from use.
+    auto step = [&](auto jc, auto lastc, int c) {
+        constexpr int J = decltype(jc)::value;
+        constexpr bool LAST = decltype(lastc)::value;
+        if constexpr (!LAST || J + 1 < SLOTS) store_a(aset[(J + 1) % SLOTS], (c + 1) & 1);  // buffer of step c - 1
+        if constexpr (!LAST) load_a(aset[J], c + SLOTS);
+        if constexpr (!LAST || J + kWrAhead < SLOTS) load_w(wv[(J + kWrAhead) % SLOTS], c + kWrAhead);
+        const uint8_t *st = ring[c & 1];
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            if (16 * q < rows) {  // wave-uniform: the row group holds list entries
+                const int r = 16 * q + (lane & 15);
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const int g = 4 * s2 + (lane >> 4);
+                    const int off = r * ROWB + 16 * (g ^ ((r >> 1) & 7));
+                    const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + off));
+                    const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + ABYTES + off));
+                    const bf16x8 bv = __builtin_bit_cast(bf16x8, wv[J][s2]);
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, acc[q], 0, 0, 0);
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, acc[q], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    static_assert(SLOTS == 4 && kWrAhead == 3, "one step call per slot below");
+    // prologue, in the steady state's order: activations and weights of steps 0..2, activations of 3
+    load_a(aset[0], 0);
+    load_w(wv[0], 0);
+    load_a(aset[1], 1);
+    load_w(wv[1], 1);
+    load_a(aset[2], 2);
+    load_w(wv[2], 2);
+    load_a(aset[3], 3);
+    store_a(aset[0], 0);
+    __syncthreads();
+    int c0 = 0;
+    for (; c0 + SLOTS < nch; c0 += SLOTS) {
+        step(I0{}, std::false_type{}, c0);
+        step(I1{}, std::false_type{}, c0 + 1);
+        step(I2{}, std::false_type{}, c0 + 2);
+        step(I3{}, std::false_type{}, c0 + 3);
+    }
+    step(I0{}, std::true_type{}, c0);
+    step(I1{}, std::true_type{}, c0 + 1);
+    step(I2{}, std::true_type{}, c0 + 2);
+    step(I3{}, std::true_type{}, c0 + 3);
+
+    // epilogue: acc[q] lane holds tile row 16 W + (lane % 16) for list rows 16 q + 4*(lane/16) + i. Gate/up:
+    // the W3 waves hand their sums to the W1 wave of the same columns through the (idle) ring.
+    if constexpr (MATS == 2) {
+        f32x4 *xch = reinterpret_cast<f32x4 *>(&ring[0][0]);  // [W - 8][q][lane]
+        if (W >= kWrWaves / 2) {
+#pragma unroll
+            for (int q = 0; q < RG; ++q)
+                if (16 * q < rows) xch[((W - kWrWaves / 2) * RG + q) * 64 + lane] = acc[q];
+        }
+        __syncthreads();
+        if (W >= kWrWaves / 2) return;
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            if (16 * q >= rows) break;
+            const f32x4 up = xch[(W * RG + q) * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * q + 4 * (lane >> 4) + i;
+                if (r >= rows) continue;
+                const float g = acc[q][i], u = up[i];
+                const float v = (g / (1.0f + expf(-g))) * u;  // silu(g) * u, rabbit2.c:535-537
+                const uint32_t hb = f32_to_bf16_rne(v);
+                const uint32_t lb = f32_to_bf16_rne(v - __uint_as_float(hb << 16));
+                const size_t o = (size_t)(row0 + r) * N + n0 + 16 * W + (lane & 15);
+                out_hi[o] = (uint16_t)hb;
+                out_lo[o] = (uint16_t)lb;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            if (16 * q >= rows) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * q + 4 * (lane >> 4) + i;
+                if (r >= rows) continue;
+                out_f32[(size_t)(row0 + r) * N + n0 + 16 * W + (lane & 15)] = acc[q][i];
+            }
+        }
+    }
+}
+
+// The grouped GEMM of the 64- and 128-row tiles in one launch: the dispatch kernel chose the tile
+// height from the histogram (*choice: 1 = 128-row tiles over m_off128, 0 = 64-row tiles over m_off64),
+// and every block runs that path on its tile slot. Both paths take 16 waves; the LDS is the larger
+// ring (the 64-row tiles').
+constexpr int kSelLds = GTile<64, 256>::kStages * GTile<64, 256>::kStageBytes;
+static_assert(kSelLds >= 2 * 2 * kWrRows * 2 * kWrKC && GTile<64, 256>::kWaves == kWrWaves, "shared launch shape");
+template <int MATS>
+__global__ __launch_bounds__(64 * kWrWaves, 1) void grouped_gemm_sel_kernel(
+    const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
+    int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ m_off64, const int32_t *__restrict__ m_off128, const int32_t *__restrict__ choice,
+    int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi, uint16_t *__restrict__ out_lo,
+    const uint8_t *__restrict__ tiled, uint64_t tiled_stride, uint64_t tiled_off) {
+    __shared__ __align__(1024) uint8_t smem[kSelLds];
+    if (__builtin_amdgcn_readfirstlane(*choice))
+        gemm_wr_tile<MATS>(smem, blockIdx.x, experts, stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk,
+                           counts, offsets, m_off128, E, out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
+    else
+        gemm_lds_tile<MATS, 64, 256>(smem, (uint32_t)(uintptr_t)smem, blockIdx.x, experts, stride, w_off, w3_off, N,
+                                     Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, E, out_f32, out_hi,
+                                     out_lo);
+}
+
 // moe[t][d] = sum_k w[t][k] * y[pos_of[t*K+k]][d] in selection order (rabbit2.c:540); x += moe.
 __global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restrict__ y,
                                                           const int32_t *__restrict__ pos_of,
@@ -415,20 +749,54 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restri
     if (x_inout) x_inout[o] = xo + moe;
 }
 
-template <int MATS, int ROWS>
+template <int MATS, int ROWS, int WROWS>
 hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
                        int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
                        int topk, const int32_t *counts, const int32_t *offsets, const int32_t *m_off, int E,
                        int max_mtiles, float *out_f32, uint16_t *out_hi, uint16_t *out_lo) {
-    const long long tiles = (long long)max_mtiles * (N / (GTile<ROWS>::kWRows / MATS));
+    if (N % (WROWS / MATS) != 0) return hipErrorInvalidValue;
+    const long long tiles = (long long)max_mtiles * (N / (WROWS / MATS));
     const long long blocks = (tiles + 7) / 8 * 8;
     if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
-    return launch(L, grouped_gemm_kernel<MATS, ROWS>, dim3((unsigned)blocks), dim3(64 * GTile<ROWS>::kWaves), 0, experts,
-                  stride, w_off, w3_off,
-                  N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, out_f32, out_hi, out_lo);
+    return launch(L, grouped_gemm_kernel<MATS, ROWS, WROWS>, dim3((unsigned)blocks), dim3(64 * GTile<ROWS, WROWS>::kWaves),
+                  0, experts, stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E,
+                  out_f32, out_hi, out_lo);
+}
+
+template <int MATS>
+hipError_t launch_gemm_sel(const Launch &L, const uint8_t *experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
+                           int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
+                           int topk, const int32_t *counts, const int32_t *offsets, const int32_t *m_off64,
+                           const int32_t *m_off128, const int32_t *choice, int E, int max_mtiles64, float *out_f32,
+                           uint16_t *out_hi, uint16_t *out_lo, const uint8_t *tiled, uint64_t tiled_stride,
+                           uint64_t tiled_off) {
+    constexpr int NTILE = MATS == 2 ? 128 : 256;  // both paths' tile width
+    static_assert(NTILE == 256 / MATS, "the 64-row tiles are as wide");
+    if (!gemm_wr_supported(MATS, N, Kd)) return hipErrorInvalidValue;
+    const long long tiles = (long long)max_mtiles64 * (N / NTILE);  // >= the 128-row tiles
+    const long long blocks = (tiles + 7) / 8 * 8;
+    if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
+    return launch(L, grouped_gemm_sel_kernel<MATS>, dim3((unsigned)blocks), dim3(64 * kWrWaves), 0, experts, stride,
+                  w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, m_off128, choice, E,
+                  out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
 }
 
 }  // namespace
+
+bool prefill_layout_supported(int dtype, int D, int H) {
+    return dtype == RBT_DT_BF16 && D % kGWRows == 0 && gemm_wr_supported(2, H, D) && gemm_wr_supported(1, D, H);
+}
+
+size_t prefill_layout_bytes(int E, int D, int H) { return (size_t)E * 3 * H * D * 2; }
+
+hipError_t launch_prefill_layout(const Launch &L, const void *experts, uint64_t stride, int E, int D, int H, void *dst) {
+    if (!prefill_layout_supported(RBT_DT_BF16, D, H) || E < 1 || E > 65535 || stride % 16 != 0 ||
+        (reinterpret_cast<uintptr_t>(experts) & 15u) || (reinterpret_cast<uintptr_t>(dst) & 15u))
+        return hipErrorInvalidValue;
+    const uint64_t units = 3 * (uint64_t)H * D / 8;  // 16-byte units per expert
+    return launch(L, prefill_layout_kernel, dim3((unsigned)((units + 255) / 256), (unsigned)E), dim3(256), 0,
+                  static_cast<const uint8_t *>(experts), stride, D, H, static_cast<uint8_t *>(dst), units);
+}
 
 bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, int H, const void *experts, uint64_t stride,
                        const float *xb) {
@@ -441,14 +809,14 @@ bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, in
 size_t prefill_workspace_bytes(int T, int E, int K, int D) {
     const size_t P = (size_t)T * K;
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
-    return up(4 * (size_t)E) + 2 * up(4 * (size_t)(E + 1)) + 2 * up(4 * P) + up(4 * P * (size_t)D) +
+    return up(4 * (size_t)E) + 3 * up(4 * (size_t)(E + 1)) + up(4) + 2 * up(4 * P) + up(4 * P * (size_t)D) +
            2 * up(2 * (size_t)T * D);
 }
 
 namespace {
 // Workspace carve-up of the grouped path (prefill_workspace_bytes is its total).
 struct PrefillWs {
-    int32_t *counts, *offsets, *m_off, *perm, *pos_of;
+    int32_t *counts, *offsets, *m_off, *m_off128, *choice, *perm, *pos_of;
     float *y;
     uint16_t *x_hi, *x_lo;
 };
@@ -464,6 +832,8 @@ PrefillWs carve_ws(void *ws, int T, int E, int K, int D) {
     r.counts = reinterpret_cast<int32_t *>(carve(4 * (size_t)E));
     r.offsets = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
     r.m_off = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
+    r.m_off128 = reinterpret_cast<int32_t *>(carve(4 * (size_t)(E + 1)));
+    r.choice = reinterpret_cast<int32_t *>(carve(4));
     r.perm = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
     r.pos_of = reinterpret_cast<int32_t *>(carve(4 * (size_t)P));
     r.y = reinterpret_cast<float *>(carve(4 * (size_t)P * D));
@@ -488,7 +858,8 @@ void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uin
 hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
-                          int32_t **counts_out, bool x_split_done, bool combine) {
+                          int32_t **counts_out, bool x_split_done, bool combine, int tile_rows, const void *tiled) {
+    if (tile_rows != 0 && tile_rows != 32 && tile_rows != 64 && tile_rows != 128) return hipErrorInvalidValue;
     const int P = T * K;
     const PrefillWs r = carve_ws(ws, T, E, K, D);
     int32_t *counts = r.counts, *offsets = r.offsets, *m_off = r.m_off, *perm = r.perm, *pos_of = r.pos_of;
@@ -510,26 +881,46 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
         e = launch(Ls, split_hilo_kernel, dim3(sblocks), dim3(256), 0, xb, n8, x_hi, x_lo);
         if (e != hipSuccess) return e;
     }
-    // row tiles of 32 when experts average at most 16 rows (decode-sized batches: a deeper copy ring),
-    // of 64 otherwise (fewer tiles, each weight tile read once per 64 rows)
-    const bool small = P <= kSmallTileRowsPerExpert * E;
+    // Row tiles of 32 when experts average at most 16 rows (decode-sized batches: a deeper copy ring);
+    // otherwise 64-row tiles or, where the shape allows, 128-row tiles (a weight tile streamed once for
+    // up to 128 rows, by the register kernel), the dispatch kernel choosing between the two from the
+    // histogram (tile_rows 64 / 128 forces one).
+    // the 128-row kernel addresses the gathered x planes with 32-bit buffer offsets
+    const bool tall_ok = gemm_wr_supported(2, H, D) && gemm_wr_supported(1, D, H) &&
+                         (size_t)T * D * 2 + 2 * (size_t)D < (size_t)kWrBufRecords;
+    const bool small = tile_rows == 32 || (tile_rows == 0 && P <= kSmallTileRowsPerExpert * E);
     const int mt_rows = small ? 32 : 64;
+    const int tall = !tall_ok || small ? 1 : (tile_rows == 128 ? 2 : (tile_rows == 64 ? 1 : 0));
+    const bool sel = !small && tall_ok;
     e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off,
-               mt_rows);
+               mt_rows, sel ? r.m_off128 : nullptr, r.choice, tall);
     if (e != hipSuccess) return e;
     const uint8_t *ex = static_cast<const uint8_t *>(experts);
     const int max_mtiles = (P + mt_rows - 1) / mt_rows + E;  // >= sum over experts of ceil(count / mt_rows)
+    const uint64_t w3 = (uint64_t)H * D * 2, w2 = 2 * (uint64_t)H * D * 2;
+    const uint8_t *tl = static_cast<const uint8_t *>(tiled);
+    const uint64_t tstride = 3 * (uint64_t)H * D * 2;  // the tiled copy's bytes per expert
     // gate/up: N = H, Kd = D, activation rows gathered through perm; h written as hi/lo planes
-    e = small ? launch_gemm<2, 32>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets,
-                                   m_off, E, max_mtiles, nullptr, h_hi, h_lo)
-              : launch_gemm<2, 64>(Lg, ex, stride, 0, (uint64_t)H * D * 2, H, D, x_hi, x_lo, 1, perm, K, counts, offsets,
-                                   m_off, E, max_mtiles, nullptr, h_hi, h_lo);
+    if (small)
+        e = launch_gemm<2, 32, 128>(Lg, ex, stride, 0, w3, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, E,
+                                    max_mtiles, nullptr, h_hi, h_lo);
+    else if (!sel)
+        e = launch_gemm<2, 64, 256>(Lg, ex, stride, 0, w3, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, E,
+                                    max_mtiles, nullptr, h_hi, h_lo);
+    else
+        e = launch_gemm_sel<2>(Lg, ex, stride, 0, w3, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, r.m_off128,
+                               r.choice, E, max_mtiles, nullptr, h_hi, h_lo, tl, tstride, 0);
     if (e != hipSuccess) return e;
     // down: N = D, Kd = H, activation rows = the h planes in list order
-    e = small ? launch_gemm<1, 32>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts,
-                                   offsets, m_off, E, max_mtiles, y, nullptr, nullptr)
-              : launch_gemm<1, 64>(Lw, ex, stride, 2 * (uint64_t)H * D * 2, 0, D, H, h_hi, h_lo, 0, perm, K, counts,
-                                   offsets, m_off, E, max_mtiles, y, nullptr, nullptr);
+    if (small)
+        e = launch_gemm<1, 32, 128>(Lw, ex, stride, w2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets, m_off, E,
+                                    max_mtiles, y, nullptr, nullptr);
+    else if (!sel)
+        e = launch_gemm<1, 64, 256>(Lw, ex, stride, w2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets, m_off, E,
+                                    max_mtiles, y, nullptr, nullptr);
+    else
+        e = launch_gemm_sel<1>(Lw, ex, stride, w2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets, m_off, r.m_off128,
+                               r.choice, E, max_mtiles, y, nullptr, nullptr, tl, tstride, w2);
     if (e != hipSuccess) return e;
     if (!combine) return hipSuccess;
     return launch(Lc, combine_rows_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)T), dim3(256), 0,

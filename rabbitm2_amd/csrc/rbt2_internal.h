@@ -156,12 +156,19 @@ bool prefill_supported(int dtype, int T, int min_tokens, int E, int K, int D, in
                        uint64_t stride, const float *xb);
 size_t prefill_workspace_bytes(int T, int E, int K, int D);
 // x_split_done: the bf16 hi/lo planes of xb are already in the workspace (prefill_x_planes), written
-// by launch_router_prefill.
+// by launch_router_prefill. tile_rows: list rows per GEMM tile (32, 64 or 128; 0 = chosen from the
+// mean rows per expert).
 hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
                           int32_t **counts_out, bool x_split_done,
-                          bool combine = true);
+                          bool combine = true, int tile_rows = 0, const void *tiled = nullptr);
+// The tiled copy of a layer's bf16 experts that the 128-row grouped GEMMs stream contiguously (same
+// bytes as the blobs, in tile order): whether the shape has one, its size, and the re-layout launch
+// (experts in the blob layout with stride, into dst). tiled = that copy, or nullptr for the blobs.
+bool prefill_layout_supported(int dtype, int D, int H);
+size_t prefill_layout_bytes(int E, int D, int H);
+hipError_t launch_prefill_layout(const Launch &L, const void *experts, uint64_t stride, int E, int D, int H, void *dst);
 void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uint16_t **x_lo);
 // combine = false: launch_prefill stops after the down GEMM; the combine's inputs (y [P][D] in list
 // order, pos_of [P]) are then these, for launch_combine_rmsnorm.

@@ -24,7 +24,7 @@ EXPORTS = (
     "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
     "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling", "rbt_hip_file_info",
     "rbt_hip_generate_stream", "rbt_hip_routing_history", "rbt_hip_expert_cache_replay",
-    "rbt_hip_moe_dev_noalloc",
+    "rbt_hip_moe_dev_noalloc", "rbt_hip_prefill_layout", "rbt_hip_prefill_layout_drop",
 )
 
 TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32)
@@ -68,6 +68,8 @@ def lib():
         L.rbt_hip_moe_dev.argtypes = [vp, C.POINTER(MoeLayer), vp, i32, vp, vp, vp, vp]
         L.rbt_hip_moe_dev_noalloc.argtypes = [vp, C.POINTER(MoeLayer), vp, i32, vp, vp, vp, vp]
         L.rbt_hip_reserve.argtypes = [vp, C.POINTER(MoeLayer), i32]
+        L.rbt_hip_prefill_layout.argtypes = [vp, C.POINTER(MoeLayer)]
+        L.rbt_hip_prefill_layout_drop.argtypes = [vp, C.POINTER(MoeLayer)]
         L.rbt_hip_expert_counts_dev.argtypes, L.rbt_hip_expert_counts_dev.restype = [vp], vp
         L.rbt_hip_matvec.argtypes = [vp, vp, u64, vp, i32, i32]
         L.rbt_hip_matvec_dev.argtypes = [vp, vp, vp, i32, vp, i32, i32]
@@ -343,6 +345,13 @@ class Device:
 
     def reserve(self, layer, max_tokens):
         self._check(self.L.rbt_hip_reserve(self.h, C.byref(layer), max_tokens))
+
+    def prefill_layout(self, layer=None):
+        """The tiled copy of `layer`'s experts for the grouped GEMMs (None: every layer of the model)."""
+        self._check(self.L.rbt_hip_prefill_layout(self.h, None if layer is None else C.byref(layer)))
+
+    def prefill_layout_drop(self, layer=None):
+        self._check(self.L.rbt_hip_prefill_layout_drop(self.h, None if layer is None else C.byref(layer)))
 
     def expert_counts(self, n_experts):
         p = self.L.rbt_hip_expert_counts_dev(self.h)

@@ -65,11 +65,22 @@ class SynthLayer:
                             byte_offset=base + mat * esz)
             dev.fill_normal(self.experts_dev, dtype, mat, seed, po.expert_stream(cfg, layer, e, 2), scale=sc_h,
                             byte_offset=base + 2 * mat * esz)
+        self.scales = (sc_d, sc_d, sc_h)
         st = np.uint16 if dtype == po.DT_BF16 else np.float32
         self.router = dev.d2h(self.router_dev, (n_experts, dim), st)
         self.experts = dev.d2h(self.experts_dev, (n_experts * self.stride,), np.uint8)
         self.bias = None if bias is None else np.asarray(bias, np.float32)
         self.bias_dev = None if bias is None else dev.upload_array(self.bias)
+
+    def reseed_experts(self, experts, seed):
+        """Rewrites the blobs of the given experts with weights of another seed (device and host copy)."""
+        cfg = po.Config(dim=self.D, n_experts=self.E, top_k=self.K, expert_hidden=self.H, dtype=self.dtype)
+        mat = self.H * self.D
+        for e in experts:
+            for w in range(3):
+                self.dev.fill_normal(self.experts_dev, self.dtype, mat, seed, po.expert_stream(cfg, 0, e, w),
+                                     scale=self.scales[w], byte_offset=e * self.stride + w * mat * self.esz)
+        self.experts = self.dev.d2h(self.experts_dev, (self.E * self.stride,), np.uint8)
 
     def desc(self):
         from rabbitm2_amd.hip import moe_layer_desc

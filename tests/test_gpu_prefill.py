@@ -141,3 +141,114 @@ def test_grouped_not_taken_for_f32(dev, grouped_from):
 def test_prefill_min_tokens_option_checked(dev):
     with pytest.raises(Exception):
         dev.set_option("prefill_min_tokens", 0)
+
+
+@pytest.fixture
+def tile_rows(dev):
+    """Forces the grouped GEMMs' tile height; restores the choice by batch afterwards."""
+    def set_rows(n):
+        dev.set_option("prefill_tile_rows", n)
+    yield set_rows
+    dev.set_option("prefill_tile_rows", 0)
+
+
+@pytest.mark.parametrize("rows", [32, 64, 128])
+@pytest.mark.parametrize("shape", GROUPED_SHAPES[:5],
+                         ids=[f"D{s[0]}E{s[1]}K{s[2]}H{s[3]}n{s[4]}T{s[5]}" for s in GROUPED_SHAPES[:5]])
+def test_grouped_every_tile_height(dev, grouped_from, tile_rows, shape, rows):
+    """Each tile height (32, 64 or 128 list rows; 128-row tiles reduce in 32-wide steps through a
+    four-stage ring) on the grouped shapes: lists from 0 rows to a few hundred, row tiles cut short
+    at the end of each list, every expert's rows in one tile or several."""
+    D, E, K, H, nt, T = shape
+    grouped_from(1)
+    tile_rows(rows)
+    layer = SynthLayer(dev, D, E, K, H, po.DT_BF16, nt, seed=6, w_scale=1.0, fan_in=True)
+    try:
+        xb = layer.make_x(T, seed=31)
+        x = layer.make_x(T, seed=32, bf16=False)
+        check_grouped(dev, layer, xb, x=x, label=f"tile rows {rows} D{D}E{E}K{K}H{H}")
+    finally:
+        layer.close()
+
+
+@pytest.mark.parametrize("n_tok", [128, 129, 300])
+def test_grouped_tall_tiles_at_list_boundaries(dev, grouped_from, tile_rows, n_tok):
+    """128-row tiles with every token on the same 8 experts: lists of exactly one tile (128), one tile
+    and one row (129), and two full tiles plus a partial one (300); the other 56 experts are empty.
+    Deterministic from call to call."""
+    grouped_from(1)
+    tile_rows(128)
+    bias = np.zeros(64, np.float32)
+    bias[20:28] = 30.0
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=5, bias=bias)
+    try:
+        xb = layer.make_x(n_tok, seed=13)
+        got, _ = check_grouped(dev, layer, xb, label=f"tall tiles {n_tok} rows")
+        assert dev.expert_counts(64)[20:28].tolist() == [n_tok] * 8
+        again = layer.run_gpu(xb)
+        assert again["moe"].tobytes() == got["moe"].tobytes()
+    finally:
+        layer.close()
+
+
+def test_prefill_tile_rows_option_checked(dev):
+    for bad in (-1, 16, 96, 256):
+        with pytest.raises(Exception):
+            dev.set_option("prefill_tile_rows", bad)
+
+
+@pytest.mark.parametrize("rows", [64, 128])
+@pytest.mark.parametrize("biased", [False, True], ids=["uniform", "skewed"])
+def test_tiled_expert_copy_is_bitwise_the_blobs(dev, grouped_from, tile_rows, biased, rows):
+    """The OLMoE layer at 512 tokens on 64- and 128-row tiles, reading the experts from the row-major
+    blobs and from the tiled copy (rbt_hip_prefill_layout): identical outputs, both held to the oracle;
+    a dropped copy is no longer read."""
+    grouped_from(1)
+    tile_rows(rows)
+    bias = np.zeros(64, np.float32)
+    if biased:
+        bias[:8] = 2.0
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=1, bias=bias)
+    try:
+        xb = layer.make_x(512, seed=5)
+        L = layer.desc()
+        dev.prefill_layout_drop(L)
+        plain, want = check_grouped(dev, layer, xb, label="blobs")
+        dev.prefill_layout(L)
+        tiled, _ = check_grouped(dev, layer, xb, label="tiled copy")
+        assert tiled["moe"].tobytes() == plain["moe"].tobytes()
+        assert np.array_equal(tiled["routing"], plain["routing"])
+        dev.prefill_layout_drop(L)
+        again = layer.run_gpu(xb)
+        assert again["moe"].tobytes() == plain["moe"].tobytes()
+    finally:
+        dev.prefill_layout_drop()
+        layer.close()
+
+
+def test_tiled_copy_follows_changed_blobs(dev, grouped_from, tile_rows):
+    """A copy taken before the blobs change is stale until it is taken again (the documented contract):
+    after the weights of two experts are rewritten and the copy re-taken, the output matches the
+    oracle on the new weights."""
+    grouped_from(1)
+    tile_rows(128)
+    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=3)
+    try:
+        xb = layer.make_x(512, seed=7)
+        L = layer.desc()
+        dev.prefill_layout(L)
+        layer.reseed_experts([5, 40], seed=99)
+        dev.prefill_layout(L)
+        check_grouped(dev, layer, xb, label="re-taken copy")
+    finally:
+        dev.prefill_layout_drop()
+        layer.close()
+
+
+def test_prefill_layout_rejects_shapes_without_one(dev):
+    layer = SynthLayer(dev, 768, 64, 8, 384, po.DT_BF16, 0, seed=6)
+    try:
+        with pytest.raises(Exception, match="no tiled layout"):
+            dev.prefill_layout(layer.desc())
+    finally:
+        layer.close()
