@@ -73,9 +73,6 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *                         q/k/v, wo and lm_head for up to 64 sequences on the matrix cores (bf16
  *                         weights; activations as bf16 hi + lo parts, exact products); 0: VALU dot
  *                         products. Both agree with the engine to rounding.
- *   "attn_last_merge"     1 (default): where attention splits a head's positions over several blocks
- *                         (head_dim 128), the last block of each head to finish merges the partials;
- *                         0: a separate merge launch. Bit-identical results.
  *   "routing_history"     0 (default) / 1: from the next rbt_hip_state_init / rbt_hip_batch_init on,
  *                         every forward step also records its routing per sequence and position (one
  *                         small launch per step) for rbt_hip_routing_history.

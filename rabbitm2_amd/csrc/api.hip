@@ -79,7 +79,6 @@ struct DecodeState {
     float *kc = nullptr, *vc = nullptr;  // [n_seq][n_layers][ctx][kv_dim]
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr;
     float *part = nullptr;        // attention split partials [n_heads][S][hd + 2]
-    int *acnt = nullptr;          // split blocks finished per (sequence, head), zero between steps
     uint16_t *xh = nullptr, *xl = nullptr;  // bf16 hi/lo matrix-core planes of n_seq rows of max(dim, q_dim)
     float2 *rope_cs = nullptr;    // [ctx][hd/2] (cos, sin) of the RoPE angles
     float2 *cand = nullptr;       // lm_head blocks' argmax candidates
@@ -127,7 +126,6 @@ struct rbt_hip {
     Profile prof;
     int fused_decode = 1;  // option "fused_decode": batch-1 top-k inside the gate/up kernel
     int batch_mfma = 1;    // option "batch_mfma": batched dense matvecs on the matrix cores
-    int attn_last_merge = 1;  // option "attn_last_merge": split attention merged by its last block
     Sampling sampling;     // rbt_hip_set_sampling: how rbt_hip_generate* pick tokens
     uint64_t seed = 0;
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
@@ -674,20 +672,15 @@ int enqueue_step(rbt_hip *h, bool final) {
         float *const no_out[3] = {nullptr, nullptr, nullptr};
         const int wo_rows[3] = {D, 0, 0};
         const bool wo_mfma = B > 1 && h->batch_mfma && dense_mfma_supported(c.dtype, B, qd, Wo, wo_rows);
+        const bool direct = ds.S == 1;  // one split: the attention kernel writes ao (and the planes) itself
         const size_t cache = (size_t)l * ds.ctx * kvd, seq_stride = (size_t)c.n_layers * ds.ctx * kvd;
-        // one split, or several merged by the last block of each head: the attention kernel writes ao (and
-        // the planes) itself
-        const bool last_merge = ds.S > 1 && h->attn_last_merge &&
-                                 attn_last_merge_supported(hd, kvd, seq_stride, ds.kc + cache, ds.vc + cache);
-        const bool direct = ds.S == 1 || last_merge;
         STEP_LAUNCH(kProfAttn,
                     launch_attention(L, ds.q, ds.k, ds.v,
                                      c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.q_norm) : ds.q,
                                      c.qk_norm ? reinterpret_cast<const float *>(h->model + ly.k_norm) : ds.k,
                                      c.qk_norm, c.rms_eps, c.n_heads, c.n_kv_heads, hd, ds.S, ds.st, ds.kc + cache,
                                      ds.vc + cache, seq_stride, ds.rope_cs, ds.part, B, direct ? ds.ao : nullptr,
-                                     direct && wo_mfma ? ds.xh : nullptr, direct && wo_mfma ? ds.xl : nullptr,
-                                     last_merge ? ds.acnt : nullptr));
+                                     direct && wo_mfma ? ds.xh : nullptr, direct && wo_mfma ? ds.xl : nullptr));
         if (!direct)
             STEP_LAUNCH(kProfAttnMerge, launch_attn_merge(L, ds.part, c.n_heads, hd, ds.S, ds.ao, B,
                                                           wo_mfma ? ds.xh : nullptr, wo_mfma ? ds.xl : nullptr));
@@ -1383,8 +1376,6 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
         h->batch_mfma = value != 0;
     } else if (strcmp(name, "prefill_layout") == 0) {
         h->prefill_layout = value != 0;
-    } else if (strcmp(name, "attn_last_merge") == 0) {
-        h->attn_last_merge = value != 0;
     } else if (strcmp(name, "routing_history") == 0) {
         h->routing_history = value != 0;  // takes effect at the next rbt_hip_state_init / batch_init
     } else if (strcmp(name, "prefill_min_tokens") == 0) {
@@ -1493,7 +1484,7 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     const uint64_t o_kc = carve(4 * B * c.n_layers * ctx * kvd), o_vc = carve(4 * B * c.n_layers * ctx * kvd);
     const uint64_t o_x = carve(4 * B * D), o_xb = carve(4 * B * D), o_q = carve(4 * B * qd), o_k = carve(4 * B * kvd),
                    o_v = carve(4 * B * kvd), o_ao = carve(4 * B * qd);
-    const uint64_t o_part = carve(4 * B * c.n_heads * ds.S * (hd + 2)), o_acnt = carve(4 * B * c.n_heads);
+    const uint64_t o_part = carve(4 * B * c.n_heads * ds.S * (hd + 2));
     const uint64_t plane = B <= 64 ? (uint64_t)mfma_plane_elems((int)B, (int)(D > qd ? D : qd)) : 0;
     const uint64_t o_xh = carve(2 * plane), o_xl = carve(2 * plane);
     const uint64_t o_rope = carve(8 * (uint64_t)ctx * (hd / 2));
@@ -1514,7 +1505,6 @@ int rbt_hip_batch_init(rbt_hip *h, int n_seq, int ctx) {
     ds.v = reinterpret_cast<float *>(b + o_v);
     ds.ao = reinterpret_cast<float *>(b + o_ao);
     ds.part = reinterpret_cast<float *>(b + o_part);
-    ds.acnt = reinterpret_cast<int *>(b + o_acnt);
     ds.xh = reinterpret_cast<uint16_t *>(b + o_xh);
     ds.xl = reinterpret_cast<uint16_t *>(b + o_xl);
     ds.rope_cs = reinterpret_cast<float2 *>(b + o_rope);

@@ -551,56 +551,6 @@ __device__ __forceinline__ void attn_out_direct(float *ao, uint16_t *ao_hi, uint
     }
 }
 
-// The split partials merged by the last of a head's S blocks to finish, instead of a merge launch. Each
-// block publishes its partial (m, l, o[hd]) with device-scope stores (written through to the point of
-// coherence), waits for their completion, and counts itself in the head's counter; the block that
-// counts S merges all S partials, read with device-scope loads, exactly as attn_merge_kernel does, and
-// resets the counter for the next step. No block waits for another. acc: this thread's element of the
-// block's o (tid < hd); po: the block's partial; ph: the head's S partials.
-__device__ __forceinline__ void attn_last_merge(float *po, const float *ph, float acc, int *cnt, int S, int hd, int b,
-                                                int B, int h, int n_heads, float *ao, uint16_t *ao_hi,
-                                                uint16_t *ao_lo) {
-    __shared__ float wa[64], s_inv;
-    __shared__ int s_last;
-    const int tid = threadIdx.x;
-    if (tid < hd) __hip_atomic_store(po + 2 + tid, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores (and thread 0's m, l) are complete
-    __syncthreads();
-    if (tid == 0)
-        s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
-    __syncthreads();
-    if (!s_last) return;
-    if (tid < kWave) {  // split weights by wave 0 (S <= 64), attn_merge_kernel's arithmetic
-        const int q = tid;
-        const float m = q < S ? __hip_atomic_load(ph + (size_t)q * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : -INFINITY;
-        const float l = q < S ? __hip_atomic_load(ph + (size_t)q * (hd + 2) + 1, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : 0.0f;
-        const float M = wave_max(m);
-        const float a = l > 0.0f ? expf(m - M) : 0.0f;
-        wa[q] = a;
-        const float L = wave_sum(a * l);
-        if (q == 0) s_inv = 1.0f / L;
-    }
-    __syncthreads();
-    if (tid < hd) {
-        float o = 0.0f;
-        for (int q = 0; q < S; ++q)
-            o += wa[q] * __hip_atomic_load(ph + (size_t)q * (hd + 2) + 2 + tid, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-        const float v = o * s_inv;
-        ao[(size_t)b * n_heads * hd + (size_t)h * hd + tid] = v;
-        if (ao_hi) {
-            const size_t oi = mfma_plane_index(b, h * hd + tid, (B + 15) / 16);
-            const uint32_t hb = f32_to_bf16_rne(v);
-            ao_hi[oi] = (uint16_t)hb;
-            ao_lo[oi] = (uint16_t)f32_to_bf16_rne(v - __uint_as_float(hb << 16));
-        }
-    }
-    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int AE>
 __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_raw, const float *__restrict__ k_raw,
                                                    const float *__restrict__ v_raw, const float *__restrict__ qw,
@@ -609,7 +559,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
                                                    float *__restrict__ kc, float *__restrict__ vc, size_t seq_stride,
                                                    const float2 *__restrict__ rope_cs, float *__restrict__ part,
                                                    float *__restrict__ ao, uint16_t *__restrict__ ao_hi,
-                                                   uint16_t *__restrict__ ao_lo, int *__restrict__ cnt) {
+                                                   uint16_t *__restrict__ ao_lo) {
     __shared__ __align__(16) float qh[256], kh[256], vh[256];
     __shared__ float red[16], w_m[4], w_l[4];
     __shared__ __align__(16) float w_o[4][256];
@@ -771,27 +721,22 @@ __global__ __launch_bounds__(256) void attn_kernel(const float *__restrict__ q_r
             const float L = wave_sum(a * ls);
             if (lane == 0) {
                 g_L = L;
-                if (cnt) {  // published for the last-arriving block (attn_last_merge)
-                    __hip_atomic_store(po, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(po + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else if (!ao) {
+                if (!ao) {
                     po[0] = M;
                     po[1] = L;
                 }
             }
         }
         __syncthreads();
-        float acc = 0.0f;
         if (tid < kAttnG8Hd) {
+            float acc = 0.0f;
 #pragma unroll 8
             for (int q2 = 0; q2 < 32; ++q2) acc += g_a[q2] * g_o[q2][tid];
-            if (ao && !cnt)
+            if (ao)
                 attn_out_direct(ao, ao_hi, ao_lo, b, gridDim.z, h, hd, n_heads * hd, tid, acc, g_L);
-            else if (!cnt)
+            else
                 po[2 + tid] = acc;
         }
-        if (cnt) attn_last_merge(po, part + (size_t)h * S * (hd + 2), acc, cnt + (size_t)b * n_heads + h, S, hd, b,
-                                 gridDim.z, h, n_heads, ao, ao_hi, ao_lo);
         return;
     }
     float q[AEr], o[AEr];
@@ -1532,30 +1477,23 @@ hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
-                            float *part, int B, float *ao, uint16_t *ao_hi, uint16_t *ao_lo, int *merge_cnt) {
+                            float *part, int B, float *ao, uint16_t *ao_hi, uint16_t *ao_lo) {
     if (hd > kWave * kAttnMaxE || S > 64) return hipErrorInvalidValue;
-    if (ao && ((S != 1 && !merge_cnt) || (ao_hi == nullptr) != (ao_lo == nullptr) ||
-               (ao_hi && (B > 64 || (n_heads * hd) % 32 != 0))))
-        return hipErrorInvalidValue;
-    if (merge_cnt && (S < 2 || !ao || !attn_last_merge_supported(hd, n_kv * hd, seq_stride, kc, vc)))
+    if (ao && (S != 1 || (ao_hi == nullptr) != (ao_lo == nullptr) || (ao_hi && (B > 64 || (n_heads * hd) % 32 != 0))))
         return hipErrorInvalidValue;
     const dim3 g((unsigned)n_heads, (unsigned)S, (unsigned)B), b(256);
     const int kvd = n_kv * hd;
     if (hd == kAttnG8Hd && kvd % 4 == 0 && seq_stride % 4 == 0 && al16(kc) && al16(vc))
         return launch(L, attn_kernel<0>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo, merge_cnt);
+                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
     if (hd <= kWave)
         return launch(L, attn_kernel<1>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo, (int *)nullptr);
+                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
     if (hd <= 2 * kWave)
         return launch(L, attn_kernel<2>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo, (int *)nullptr);
+                      seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
     return launch(L, attn_kernel<kAttnMaxE>, g, b, 0, q, k, v, qw, kw, qk_norm, eps, n_heads, n_kv, hd, S, st, kc, vc,
-                  seq_stride, rope_cs, part, ao, ao_hi, ao_lo, (int *)nullptr);
-}
-
-bool attn_last_merge_supported(int hd, int kvd, size_t seq_stride, const float *kc, const float *vc) {
-    return hd == kAttnG8Hd && kvd % 4 == 0 && seq_stride % 4 == 0 && al16(kc) && al16(vc);
+                  seq_stride, rope_cs, part, ao, ao_hi, ao_lo);
 }
 
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,

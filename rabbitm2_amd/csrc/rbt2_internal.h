@@ -230,19 +230,14 @@ hipError_t launch_dense_argmax(const Launch &L, int dtype, const float *x, const
 // Attention of one step: grid (n_heads, S splits of the positions), each block writes its partial
 // (m, l, o[hd]) to part [n_heads][S][hd + 2]; launch_attn_merge merges them into ao (S <= 64). With
 // S == 1 and ao given, the attention writes ao [B][n_heads * hd] (and the matrix-core planes ao_hi /
-// ao_lo, if given) itself, bit for bit what the merge would, and no merge is launched. With S > 1, ao
-// and merge_cnt given (a zeroed int per (sequence, head), left zeroed; only where
-// attn_last_merge_supported), the last split block of each head to finish merges the S partials into
-// ao itself, bit for bit what launch_attn_merge computes, and no merge is launched either.
+// ao_lo, if given) itself, bit for bit what the merge would, and no merge is launched.
 // rope_cs: [ctx][hd/2] (cos, sin) of the engine's RoPE angles. hd <= 256.
 // kc/vc: this layer's cache of sequence 0; sequence b's starts seq_stride floats further.
 hipError_t launch_attention(const Launch &L, const float *q, const float *k, const float *v, const float *qw,
                             const float *kw, int qk_norm, float eps, int n_heads, int n_kv, int hd, int S,
                             const StepState *st, float *kc, float *vc, size_t seq_stride, const float2 *rope_cs,
                             float *part, int B,
-                            float *ao = nullptr, uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr,
-                            int *merge_cnt = nullptr);
-bool attn_last_merge_supported(int hd, int kvd, size_t seq_stride, const float *kc, const float *vc);
+                            float *ao = nullptr, uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr);
 hipError_t launch_attn_merge(const Launch &L, const float *part, int n_heads, int hd, int S, float *ao, int B,
                              uint16_t *ao_hi = nullptr, uint16_t *ao_lo = nullptr);
 // Dense rows over B token vectors xin [B][D] (batched decode): out_s [B][rows_s], or with resid != NULL

@@ -282,48 +282,3 @@ def test_deferred_profile_on_the_fused_combine_path(dev):
     for p in range(2):
         assert np.array_equal(outs[p][1][:, 0, :], wr[p])
         assert normwise_err(outs[p][0][0], wl[p]) <= LOGIT_RTOL
-
-
-@pytest.mark.parametrize("B,ctx,n", [(1, 600, 300), (1, 64, 64), (4, 1100, 200), (20, 96, 90)],
-                         ids=["bs1_16splits", "bs1_2splits", "B4_16splits_planes", "B20_3splits_planes"])
-def test_split_attention_merged_by_its_last_block(dev, B, ctx, n):
-    """The OLMoE head shape (16 heads x 128, QK-norm) with several position splits (ctx / 32, at most 16):
-    the last split block of each head to finish merges the partials itself (option attn_last_merge, the
-    default) instead of a merge launch. Both ways must give the same logits and routing bit for bit at
-    every position (B > 1 also writes the matrix-core planes of the batched wo), and the greedy ids of
-    the graph-replayed generate loop must agree; sequence 0 is also held to the oracle run on it alone."""
-    spec = MANIFEST["cases"]["olmoe_layer_bf16"]
-    cfg = po.Config(**dict(spec["config"], max_seq=2048))
-    g = spec["gen_params"]
-    model = po.build_model(cfg, po.GenParams(seed=g["seed"], w_scale=g["w_scale"], fan_in_scale=g["fan_in_scale"],
-                                             emb_scale=g["emb_scale"], norm_jitter=g["norm_jitter"]))
-    assert B * cfg.n_heads < 512 and ctx // 32 >= 2  # several splits (kAttnDirectBlocks)
-    dev.upload(model)
-    dev.set_router_order(po.ORDER_AVX2)
-    prompts = prompts_for(cfg, B, n, seed=B + ctx)
-    print(f"B={B} ctx={ctx} n={n}", flush=True)
-    runs, gens = {}, {}
-    try:
-        for mode in (1, 0):
-            dev.set_option("attn_last_merge", mode)
-            dev.batch_init(B, ctx)
-            runs[mode] = [dev.forward_batch(prompts[:, p], np.full(B, p, np.int32), cfg.vocab, cfg.n_layers,
-                                            cfg.top_k) for p in range(n)]
-            n_gen = min(16, ctx - n // 2)
-            if B == 1:
-                dev.state_init(ctx)
-                gens[mode] = dev.generate(prompts[0, :n // 2], n_gen)[0]
-            else:
-                dev.batch_init(B, ctx)
-                gens[mode] = dev.generate_batch(prompts[:, :n // 2], n_gen)[0].tolist()
-    finally:
-        dev.set_option("attn_last_merge", 1)
-    for p in range(n):
-        (l1, r1), (l0, r0) = runs[1][p], runs[0][p]
-        assert np.array_equal(r1, r0), f"pos {p}: routing"
-        assert np.array_equal(l1.view(np.uint32), l0.view(np.uint32)), f"pos {p}: logits differ"
-    assert gens[1] == gens[0]
-    wl, wr, _ = po.run(model, prompts[0], order=po.ORDER_AVX2, ctx=n)
-    for p in range(n):
-        assert np.array_equal(runs[1][p][1][:, 0, :], wr[p]), f"pos {p}"
-        assert normwise_err(runs[1][p][0][0], wl[p]) <= LOGIT_RTOL, f"pos {p}"
