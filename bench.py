@@ -163,6 +163,10 @@ def main():
         dev.synchronize()
         dev.free(src)
         dev.free(dst)
+        # calibration only: nothing else runs under the counters (and no HIP graph under the profiler)
+        print(f"copy-calib: {args.copy_calib_mib} MiB device-to-device copy", file=sys.stderr, flush=True)
+        dev.close()
+        return
 
     # ---- headline: whole-model bs=1 greedy decode
     cfg, setup_s = make_full_model(dev)
