@@ -448,12 +448,16 @@ __global__ __launch_bounds__(256) void topk_split_kernel(const float *__restrict
 
 // Prefill front end in one launch (AVX2 order, E <= 64, bf16): router logits, softmax + top-k, and the
 // bf16 hi/lo split of x for the grouped GEMMs. One block per kPTok tokens covers all router rows, so the
-// top-k runs in the block. Wave (token tl, half h) holds the 64 router rows in its lanes and runs
-// chains 8h..8h+7 of each (as the batched kernel); x is then the same for the whole wave, so it is read
-// with scalar loads and enters the multiplies as a scalar operand, and LDS only serves the router rows
-// (one 16-byte read per step and lane). Router columns stream through LDS in double-buffered chunks of
-// kPCols; each x element's hi/lo parts are written by one thread.
-constexpr int kPTok = 2, kPCols = 512, kPThreads = kPTok * 64 * 2;
+// top-k runs in the block. Wave (token tl, quarter q) holds the 64 router rows in its lanes and runs
+// chains 4q..4q+3 of each: eight waves per block, two per SIMD, since a SIMD issues two waves' VALU
+// operations in the time one wave issues one. Router columns stream through LDS in double-buffered
+// chunks of kPCols (coalesced global reads; each lane then reads its row's 8-byte slice per step). x is
+// the same for the whole wave: it is read with scalar loads, kPGroup steps at a time and one group
+// ahead, and enters the multiplies as a scalar operand, so no lane-by-lane copy of it returns from
+// memory. What bounds it at 512 tokens is the staging: every block pulls the whole 256 KiB router from
+// L2, and a CU's outstanding misses at L2 latency give it ~26 GB/s (about 10 of the kernel's 16 us);
+// the VALU work (a widen, a rounded multiply and a rounded add per weight) runs under that.
+constexpr int kPTok = 2, kPCols = 512, kPGroup = 8, kPThreads = kPTok * 64 * 4;
 template <int DT>
 __global__ __launch_bounds__(kPThreads) void router_prefill_kernel(const float *__restrict__ xb,
                                                                    const void *__restrict__ Wv,
@@ -463,25 +467,28 @@ __global__ __launch_bounds__(kPThreads) void router_prefill_kernel(const float *
                                                                    uint16_t *__restrict__ x_hi,
                                                                    uint16_t *__restrict__ x_lo) {
     static_assert(DT == RBT_DT_BF16, "bf16 router rows");
-    constexpr int CW = kPCols;          // columns per chunk (1 KiB per row)
-    constexpr int WP = CW * 2 + 32;     // row pitch in bytes (16-byte reads of 16 consecutive rows hit distinct banks)
-    constexpr int UPR = CW * 2 / 16;    // 16-byte units per row per chunk
+    constexpr int CW = kPCols;                // columns per chunk (1 KiB per row)
+    constexpr int WP = CW * 2 + 16;           // row pitch in bytes
+    constexpr int UPR = CW * 2 / 16;          // 16-byte units per row per chunk
     constexpr int WU = 64 * UPR / kPThreads;  // per thread per chunk
+    constexpr int G = kPGroup;
+    constexpr int SU = 2;                     // split: 16-byte loads in flight per thread
     __shared__ __align__(16) unsigned char wt[2][64 * WP];
-    __shared__ __align__(16) float s_part[kPTok][8][64];  // chains 8..15 of each (token, row)
+    __shared__ __align__(16) float s_part[kPTok][16][64];  // the 16 chains of each (token, row)
     __shared__ __align__(16) float s_log[kPTok][64];
     __shared__ __align__(16) float s_v[kPTok][64];
     __shared__ float s_p[kPTok][64];
     const uint16_t *Wg = static_cast<const uint16_t *>(Wv);
     const int tid = threadIdx.x, r = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-    const int h = wv & 1, tl = wv >> 1;
+    const int q = wv & 3, tl = wv >> 2;
     const int t0 = blockIdx.x * kPTok;
     const int ntok = min(kPTok, T - t0);
     const int body = (D / 16) * 16;
     const int nch = (body + CW - 1) / CW;
     const bool live = tl < ntok;  // wave-uniform
-    const float *xrow = xb + (size_t)(t0 + (live ? tl : 0)) * D + 8 * h;
+    const float *xrow = xb + (size_t)(t0 + (live ? tl : 0)) * D + 4 * q;  // wave-uniform: scalar loads
+    const float bias_r = bias ? bias[min(r, E - 1)] : 0.0f;  // read now, used at the end
 
     u32x4 wv4[WU];
     auto load = [&](int c) {
@@ -500,74 +507,116 @@ __global__ __launch_bounds__(kPThreads) void router_prefill_kernel(const float *
             *reinterpret_cast<u32x4 *>(wt[c & 1] + row * WP + k * 16) = wv4[i];
         }
     };
+    if (nch > 0) load(0);  // in flight during the split
 
-    // the hi/lo split of this block's x rows: plain loads and stores, one 16-byte unit per thread step
+    // the hi/lo split of this block's x rows (contiguous): SU 16-byte loads in flight per thread; a
+    // unit past the rows is clamped to the last one, which is then written twice with the same bytes
     if (x_hi) {
         const int units = ntok * D / 4;
-        for (int u = tid; u < units; u += kPThreads) {
-            const int tt = u / (D / 4), k = u % (D / 4);
-            const size_t o = (size_t)(t0 + tt) * D + 4 * k;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(xb + o);
-            uint32_t hb[4], lb[4];
+        const size_t base = (size_t)t0 * D;
+        for (int u0 = tid; u0 < units; u0 += SU * kPThreads) {
+            f32x4 v[SU];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t q = __float_as_uint(v[j]);
-                q += 0x7FFFu + ((q >> 16) & 1u);
-                hb[j] = q >> 16;
-                uint32_t l = __float_as_uint(v[j] - __uint_as_float(hb[j] << 16));
-                l += 0x7FFFu + ((l >> 16) & 1u);
-                lb[j] = l >> 16;
+            for (int i = 0; i < SU; ++i) v[i] = ld_f4(xb + base + 4 * (size_t)min(u0 + i * kPThreads, units - 1));
+#pragma unroll
+            for (int i = 0; i < SU; ++i) {
+                const size_t o = base + 4 * (size_t)min(u0 + i * kPThreads, units - 1);
+                uint32_t hb[4], lb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hb[j] = f32_to_bf16_rne(v[i][j]);
+                    lb[j] = f32_to_bf16_rne(v[i][j] - __uint_as_float(hb[j] << 16));
+                }
+                *reinterpret_cast<uint2 *>(x_hi + o) = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+                *reinterpret_cast<uint2 *>(x_lo + o) = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
             }
-            *reinterpret_cast<uint2 *>(x_hi + o) = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-            *reinterpret_cast<uint2 *>(x_lo + o) = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
         }
     }
 
-    float acc[8];
+    float acc[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    if (nch > 0) {
-        load(0);
-        store(0);
-    }
+    for (int j = 0; j < 4; ++j) acc[j] = 0.0f;
+    auto step = [&](const uint2 a, const float *xs) {
+        acc[0] = acc[0] + bf16_lo(a.x) * xs[0];
+        acc[1] = acc[1] + bf16_hi(a.x) * xs[1];
+        acc[2] = acc[2] + bf16_lo(a.y) * xs[2];
+        acc[3] = acc[3] + bf16_hi(a.y) * xs[3];
+    };
+    if (nch > 0) store(0);
     __syncthreads();
     for (int c = 0; c < nch; ++c) {
         const bool more = c + 1 < nch;
         if (more) load(c + 1);  // in flight during this chunk's chains
-        const int c0 = c * CW, steps = min(CW, body - c0) / 16;
-        if (live && r < E) {
-            const unsigned char *wr = wt[c & 1] + r * WP + 16 * h;
+        const int c0 = c * CW, steps = min(CW, body - c0) / 16, full = steps / (2 * G) * (2 * G);
+        if (live) {  // every lane (rows past E repeat row E - 1 and are not used): uniform control flow
+            const unsigned char *wr = wt[c & 1] + r * WP + 8 * q;
             const float *xc = xrow + c0;
-#pragma unroll 8
-            for (int m = 0; m < steps; ++m) {
-                const u32x4 a = *reinterpret_cast<const u32x4 *>(wr + 32 * m);
-                const float *xs = xc + 16 * m;  // wave-uniform: scalar loads
-                acc[0] = acc[0] + bf16_lo(a.x) * xs[0];
-                acc[1] = acc[1] + bf16_hi(a.x) * xs[1];
-                acc[2] = acc[2] + bf16_lo(a.y) * xs[2];
-                acc[3] = acc[3] + bf16_hi(a.y) * xs[3];
-                acc[4] = acc[4] + bf16_lo(a.z) * xs[4];
-                acc[5] = acc[5] + bf16_hi(a.z) * xs[5];
-                acc[6] = acc[6] + bf16_lo(a.w) * xs[6];
-                acc[7] = acc[7] + bf16_hi(a.w) * xs[7];
+            // groups of G steps in two register sets: while one set's group multiplies, the other set
+            // takes the next group's router slices (LDS) and x (scalar loads at constant offsets from
+            // one base, so few address registers). The fetch after the last group is clamped into the
+            // chunk and its values are not used. A scalar-load wait cannot skip the newest loads (they
+            // return out of order), so each fetch is issued only once the set about to multiply has
+            // arrived: its offset takes a register-only dependence on that set's first value (an empty
+            // asm), which places the wait before it; scheduling barriers keep each fetch ahead of the
+            // other set's multiplies.
+            uint2 wa[G], wb[G];
+            float xa[G * 4], xb4[G * 4];
+            auto fetch = [&](uint2 (&w)[G], float (&x)[G * 4], int g, float after) {
+                g = min(g, steps - G);
+                int xo = 16 * g;
+                asm volatile("" : "+s"(xo) : "s"(after));
+                const unsigned char *wp = wr + 32 * g;
+                const float *xp = xc + xo;
+#pragma unroll
+                for (int i = 0; i < G; ++i) w[i] = *reinterpret_cast<const uint2 *>(wp + 32 * i);
+#pragma unroll
+                for (int k = 0; k < G * 4; ++k) x[k] = xp[16 * (k / 4) + k % 4];
+            };
+            // all of a group's products first, then its adds in step order: dependent operations sit
+            // far apart, so neither wave of a SIMD waits on a result
+            auto run = [&](const uint2 (&w)[G], const float (&x)[G * 4]) {
+                float pr[G][4];
+#pragma unroll
+                for (int i = 0; i < G; ++i) {
+                    pr[i][0] = bf16_lo(w[i].x) * x[4 * i];
+                    pr[i][1] = bf16_hi(w[i].x) * x[4 * i + 1];
+                    pr[i][2] = bf16_lo(w[i].y) * x[4 * i + 2];
+                    pr[i][3] = bf16_hi(w[i].y) * x[4 * i + 3];
+                }
+#pragma unroll
+                for (int i = 0; i < G; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] = acc[j] + pr[i][j];
+            };
+            if (full > 0) fetch(wa, xa, 0, 0.0f);
+            for (int g = 0; g < full; g += 2 * G) {
+                fetch(wb, xb4, g + G, xa[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                run(wa, xa);
+                __builtin_amdgcn_sched_barrier(0);
+                fetch(wa, xa, g + 2 * G, xb4[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                run(wb, xb4);
+                __builtin_amdgcn_sched_barrier(0);
             }
+            for (int m = full; m < steps; ++m) step(*reinterpret_cast<const uint2 *>(wr + 32 * m), xc + 16 * m);
         }
         if (more) store(c + 1);  // the other buffer: last read in chunk c-1, before the barrier below
         __syncthreads();
     }
-    if (h == 1 && live) {
+    if (live) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s_part[tl][j][r] = acc[j];
+        for (int j = 0; j < 4; ++j) s_part[tl][4 * q + j][r] = acc[j];
     }
     __syncthreads();
-    if (h == 0 && live && r < E) {
-        float sum = 0.0f;  // the engine's lanes a[j] + b[j], summed from j = 0
+    if (q == 0 && live && r < E) {
+        float sum = 0.0f;  // the engine's lanes a[j] + b[j] (chains j and 8 + j), summed from j = 0
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sum = sum + (acc[j] + s_part[tl][j][r]);
+        for (int j = 0; j < 8; ++j) sum = sum + (s_part[tl][j][r] + s_part[tl][8 + j][r]);
         const uint16_t *wrow = Wg + (size_t)r * D;
         const float *x = xb + (size_t)(t0 + tl) * D;
         for (int i = body; i < D; ++i) sum = sum + widen<DT>(wrow[i]) * x[i];
-        if (bias) sum = sum + bias[r];
+        if (bias) sum = sum + bias_r;
         s_log[tl][r] = sum;
     }
     __syncthreads();
