@@ -37,6 +37,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kDispatchMaxE = 256;
+constexpr int kDispRegs = 4;  // 64-pair steps per wave kept in registers by dispatch_kernel (4096 pairs)
 
 
 // ---------------------------------------------------------------- dispatch (one block, 1024 threads)
@@ -49,9 +50,10 @@ constexpr int kDispatchMaxE = 256;
 // one, measured on the OLMoE layer at 512 tokens with uniform and skewed routing).
 // Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
 // equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
-// row; a pair's rank inside its wave's slice goes to pos_of as a temporary. B: wave 0 (4 experts per
-// lane) sums the waves' counts, scans them into the offsets, and turns each wave's counts into that
-// wave's first position per expert. C: every pair adds its wave's base. Three barriers in all.
+// row; a pair's rank inside its wave's slice stays in a register (pos_of holds it past the first
+// kDispRegs steps). B: wave 0 (4 experts per lane) sums the waves' counts, scans them into the
+// offsets, and turns each wave's counts into that wave's first position per expert. C: every pair
+// adds its wave's base. Three barriers in all.
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ routing, int P, int E,
                                                         int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ perm, int32_t *__restrict__ pos_of,
@@ -61,15 +63,16 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
     constexpr int NW = 16;
     __shared__ int s_w[NW][kDispatchMaxE];  // A: running counts per wave; B: each wave's base positions
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int i = tid; i < NW * kDispatchMaxE; i += 1024) (&s_w[0][0])[i] = 0;
-    __syncthreads();
     const int S = ((P + NW - 1) / NW + 63) / 64 * 64;  // slice per wave, whole 64-pair steps
     const int base = wv * S, end = min(P, base + S);
+    int rv[kDispRegs];  // the first kDispRegs steps' routing, in flight while the counts are cleared
+#pragma unroll
+    for (int i = 0; i < kDispRegs; ++i) rv[i] = routing[min(base + 64 * i + lane, P - 1)];  // unconditional
+    for (int i = tid; i < NW * kDispatchMaxE; i += 1024) (&s_w[0][0])[i] = 0;
+    __syncthreads();
     const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    for (int p0 = base; p0 < end; p0 += 64) {  // wave-uniform loop
-        const int p = p0 + lane;
-        const bool valid = p < end;
-        const int e = valid ? min(max(routing[p], 0), E - 1) : 0;
+    // one 64-pair step: the rank of each pair among the wave's earlier pairs of its expert
+    auto rank_step = [&](int p, int e, bool valid) {
         uint64_t same = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -79,8 +82,24 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
         }
         const int before = __popcll(same & below);
         const int cur = valid ? s_w[wv][e] : 0;  // read by every lane before any update (in-order LDS)
-        if (valid) pos_of[p] = cur + before;
         if (valid && (same >> lane) == 1ull) s_w[wv][e] = cur + before + 1;  // last lane of its expert
+        return cur + before;
+    };
+    // the first kDispRegs steps keep expert and rank in registers (all their routing loads issued
+    // together, nothing re-read in C); later steps, for more than 16 * 64 * kDispRegs pairs, keep the
+    // rank in pos_of and read the routing again
+    int ereg[kDispRegs], rreg[kDispRegs];
+#pragma unroll
+    for (int i = 0; i < kDispRegs; ++i) ereg[i] = base + 64 * i + lane < end ? min(max(rv[i], 0), E - 1) : -1;
+#pragma unroll
+    for (int i = 0; i < kDispRegs; ++i)
+        if (base + 64 * i < end) rreg[i] = rank_step(base + 64 * i + lane, max(ereg[i], 0), ereg[i] >= 0);
+    for (int p0 = base + 64 * kDispRegs; p0 < end; p0 += 64) {  // wave-uniform loop
+        const int p = p0 + lane;
+        const bool valid = p < end;
+        const int e = valid ? min(max(routing[p], 0), E - 1) : 0;
+        const int rk = rank_step(p, e, valid);
+        if (valid) pos_of[p] = rk;
     }
     __syncthreads();
     if (wv == 0) {
@@ -139,7 +158,16 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
         }
     }
     __syncthreads();
-    for (int p0 = base; p0 < end; p0 += 64) {
+#pragma unroll
+    for (int i = 0; i < kDispRegs; ++i) {
+        const int p = base + 64 * i + lane;
+        if (ereg[i] >= 0) {
+            const int pos = s_w[wv][ereg[i]] + rreg[i];
+            perm[pos] = p;
+            pos_of[p] = pos;
+        }
+    }
+    for (int p0 = base + 64 * kDispRegs; p0 < end; p0 += 64) {
         const int p = p0 + lane;
         if (p < end) {
             const int e = min(max(routing[p], 0), E - 1);
@@ -860,6 +888,7 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
                           int32_t **counts_out, bool x_split_done, bool combine, int tile_rows, const void *tiled) {
     if (tile_rows != 0 && tile_rows != 32 && tile_rows != 64 && tile_rows != 128) return hipErrorInvalidValue;
+    if (T <= 0 || K <= 0) return hipErrorInvalidValue;  // the dispatch reads at least one pair
     const int P = T * K;
     const PrefillWs r = carve_ws(ws, T, E, K, D);
     int32_t *counts = r.counts, *offsets = r.offsets, *m_off = r.m_off, *perm = r.perm, *pos_of = r.pos_of;
