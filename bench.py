@@ -711,10 +711,10 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
         dev.profile(0)
         counts = dev.expert_counts(E)
         # the GEMMs' row tiles, by the device's rule: 32 rows while the experts average at most 16, else
-        # 128 rows where 1.4 x their count is below the count of 64-row tiles, else 64
-        n64, n128 = (int(sum((c + m - 1) // m for c in counts)) for m in (64, 128))
-        tile_rows = 32 if P <= 16 * E else (128 if 7 * n128 < 5 * n64 else 64)
+        # 128 rows, their slots column-major where some list is longer than 4x the mean
+        tile_rows = 32 if P <= 16 * E else 128
         tiles = int(sum((c + tile_rows - 1) // tile_rows for c in counts))
+        slot_order = "column-major" if tile_rows == 128 and int(counts.max()) * E > 4 * P else "expert-major"
         issued_rows = int(sum((c + 15) // 16 * 16 for c in counts))
         for kname, fl in gemm_flops.items():
             if kname in kern:
@@ -737,6 +737,7 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             "tokens_per_expert": [int(c) for c in counts],
             "tile_rows": tile_rows,
             "row_tiles": tiles,
+            "slot_order": slot_order,
         }
     dev.prefill_layout_drop(layer0)
     out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,

@@ -44,10 +44,14 @@ constexpr int kDispRegs = 4;  // 64-pair steps per wave kept in registers by dis
 // routing [P] with pair p = t*K + k. Outputs: counts[E]; offsets[E+1] (exclusive prefix of counts);
 // perm[P]: pair ids grouped by expert, increasing within an expert; pos_of[P]: inverse of perm;
 // m_off[E+1]: exclusive prefix of ceil(counts / mt_rows) (the grouped GEMMs' row tiles per expert);
-// with m_off2 given, also m_off2[E+1] for 128-row tiles and *choice, the tile height the grouped GEMMs
-// take (1: 128 rows, 0: mt_rows): tall = 2 forces 128, 1 forces mt_rows, 0 picks 128 when
-// 1.4 x its tile count is below the mt_rows tile count (a 128-row tile takes ~1.4x as long as a 64-row
-// one, measured on the OLMoE layer at 512 tokens with uniform and skewed routing).
+// with m_off2 given, also m_off2[E+1] for 128-row tiles and *choice, the grouped GEMMs' plan: bit 0 the
+// tile height (1: 128 rows, 0: mt_rows; tall = 1 forces mt_rows, else 128), bit 1 the slot order of
+// the 128-row tiles (column-major when some list is longer than 4x the mean, else expert-major; see
+// tile_of). Measured
+// on the OLMoE layer at 512 tokens: 128-row tiles beat 64-row ones with uniform routing (209 against
+// 262 us per call) and, in column-major order, with +2 on 8 experts' logits (247 against 255 us) and
+// +4 on 4 (223 against 231 us); expert-major order keeps the uniform case's activation rows in one
+// XCD's L2 per expert (209 against 214 us).
 // Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
 // equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
 // row; a pair's rank inside its wave's slice stays in a register (pos_of holds it past the first
@@ -114,6 +118,12 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
             mt[i] = (tot + mt_rows - 1) / mt_rows;
             mt2[i] = (tot + 127) / 128;
         }
+        // a list longer than 4x the mean: the slots go column-major (tile_of) so the long lists' tiles
+        // spread over the XCDs
+        int cmax = max(max(c[0], c[1]), max(c[2], c[3]));
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) cmax = max(cmax, __shfl_xor(cmax, d, 64));
+        const bool skewed = (long long)cmax * E > 4ll * P;
         // exclusive scans across the wave of the lanes' sums (4 experts per lane, ascending)
         int sc = ((c[0] + c[1]) + c[2]) + c[3], sm = ((mt[0] + mt[1]) + mt[2]) + mt[3];
         int sm2 = ((mt2[0] + mt2[1]) + mt2[2]) + mt2[3];
@@ -148,8 +158,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                 m_off[E] = om + mt[i];
                 if (m_off2) {
                     m_off2[E] = om2 + mt2[i];
-                    const int n64 = om + mt[i], n128 = om2 + mt2[i];
-                    *choice = tall == 2 ? 1 : (tall == 1 ? 0 : (int)(7 * n128 < 5 * n64));
+                    *choice = tall == 1 ? 0 : (1 | (skewed ? 2 : 0));  // 64-row tiles: expert-major
                 }
             }
             oc += c[i];
@@ -287,12 +296,42 @@ struct GTile {
 // Requirements (prefill_supported): N % (256 / MATS) == 0, Kd % 64 == 0, 16-byte aligned rows.
 // The block's work on tile slot `bid` (the kernels below pass blockIdx.x); ring: the LDS ring of
 // STAGES * SBYTES bytes at LDS offset ring0.
+// Tile slot tau -> (expert e, column tile jt, row tile il of e's list), with m_off the prefix of the
+// experts' row tiles and nt column tiles. Expert-major (colmajor 0): e's tiles are consecutive, so an
+// expert's column tiles share its activation rows in one XCD's L2. Column-major (1): tau = jt * M + rt
+// over the M row tiles of all experts, so each XCD's contiguous share of the slots spans every
+// expert's row tiles for a few column tiles and a few long lists load all XCDs alike. Either way an
+// expert's row tiles of one column tile (one weight tile) are consecutive, on one XCD.
+__device__ __forceinline__ void tile_of(int tau, const int32_t *__restrict__ m_off, int E, int nt, int colmajor,
+                                        int *e_out, int *jt_out, int *il_out) {
+    const int M = m_off[E];
+    const int jc = colmajor ? tau / M : 0, key = colmajor ? tau - jc * M : tau, scale = colmajor ? 1 : nt;
+    int lo = 0, hi = E - 1;  // the last e with m_off[e] * scale <= key
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (m_off[mid] * scale <= key)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const int e = lo;
+    if (colmajor) {
+        *jt_out = jc;
+        *il_out = key - m_off[e];
+    } else {
+        const int me = m_off[e + 1] - m_off[e], local = key - m_off[e] * nt;
+        *jt_out = local / me;
+        *il_out = local - *jt_out * me;
+    }
+    *e_out = e;
+}
+
 template <int MATS, int ROWS, int WROWS>
 __device__ __forceinline__ void gemm_lds_tile(
     uint8_t *ring, uint32_t ring0, unsigned bid, const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off,
     uint64_t w3_off, int N, int Kd, const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather,
     const int32_t *__restrict__ perm, int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
-    const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
+    const int32_t *__restrict__ m_off, int E, int colmajor, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
     uint16_t *__restrict__ out_lo) {
     using TS = GTile<ROWS, WROWS>;
     constexpr int NTILE = WROWS / MATS;  // output columns per tile
@@ -308,18 +347,8 @@ __device__ __forceinline__ void gemm_lds_tile(
     const int slot = (int)(bid >> 3);
     const int tau = (int)(bid & 7) * range + slot;
     if (slot >= range || tau >= total) return;
-    int lo = 0, hi = E - 1;  // the expert owning tile tau: the last e with m_off[e] * ntiles_n <= tau
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (m_off[mid] * ntiles_n <= tau)
-            lo = mid;
-        else
-            hi = mid - 1;
-    }
-    const int e = lo;
-    const int me = m_off[e + 1] - m_off[e];
-    const int local = tau - m_off[e] * ntiles_n;
-    const int jt = local / me, il = local - jt * me;
+    int e, jt, il;
+    tile_of(tau, m_off, E, ntiles_n, colmajor, &e, &jt, &il);
     const int row0 = offsets[e] + il * ROWS;
     const int rows = __builtin_amdgcn_readfirstlane(min(ROWS, counts[e] - il * ROWS));  // uniform: scalar branches below
     const int n0 = jt * NTILE;
@@ -452,7 +481,7 @@ __global__ __launch_bounds__((64 * GTile<ROWS, WROWS>::kWaves), 1) void grouped_
     uint16_t *__restrict__ out_lo) {
     __shared__ __align__(1024) uint8_t ring[GTile<ROWS, WROWS>::kStages * GTile<ROWS, WROWS>::kStageBytes];
     gemm_lds_tile<MATS, ROWS, WROWS>(ring, (uint32_t)(uintptr_t)ring, blockIdx.x, experts, stride, w_off, w3_off, N,
-                                     Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, out_f32, out_hi,
+                                     Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off, E, 0, out_f32, out_hi,
                                      out_lo);
 }
 
@@ -516,7 +545,7 @@ __device__ __forceinline__ void gemm_wr_tile(
     uint8_t *smem, unsigned bid, const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
     int N, int Kd, const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather,
     const int32_t *__restrict__ perm, int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
-    const int32_t *__restrict__ m_off, int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
+    const int32_t *__restrict__ m_off, int E, int colmajor, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi,
     uint16_t *__restrict__ out_lo, const uint8_t *__restrict__ tiled, uint64_t tiled_stride, uint64_t tiled_off) {
     constexpr int NT = 64 * kWrWaves;             // threads
     constexpr int NTILE = MATS == 2 ? 128 : 256;  // output columns per tile
@@ -534,18 +563,8 @@ __device__ __forceinline__ void gemm_wr_tile(
     const int slot = (int)(bid >> 3);
     const int tau = (int)(bid & 7) * range + slot;
     if (slot >= range || tau >= total) return;
-    int lo = 0, hi = E - 1;  // the expert owning tile tau: the last e with m_off[e] * ntiles_n <= tau
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (m_off[mid] * ntiles_n <= tau)
-            lo = mid;
-        else
-            hi = mid - 1;
-    }
-    const int e = lo;
-    const int me = m_off[e + 1] - m_off[e];
-    const int local = tau - m_off[e] * ntiles_n;
-    const int jt = local / me, il = local - jt * me;
+    int e, jt, il;
+    tile_of(tau, m_off, E, ntiles_n, colmajor, &e, &jt, &il);
     const int row0 = offsets[e] + il * kWrRows;
     const int rows = __builtin_amdgcn_readfirstlane(min(kWrRows, counts[e] - il * kWrRows));
     const int n0 = jt * NTILE;
@@ -715,8 +734,9 @@ __device__ __forceinline__ void gemm_wr_tile(
 }
 
 // The grouped GEMM of the 64- and 128-row tiles in one launch: the dispatch kernel chose the tile
-// height from the histogram (*choice: 1 = 128-row tiles over m_off128, 0 = 64-row tiles over m_off64),
-// and every block runs that path on its tile slot. Both paths take 16 waves; the LDS is the larger
+// height and slot order from the histogram (*choice bit 0: 128-row tiles over m_off128, else 64-row
+// tiles over m_off64; bit 1: column-major slot order, see tile_of), and every block runs that path on
+// its tile slot. Both paths take 16 waves; the LDS is the larger
 // ring (the 64-row tiles').
 constexpr int kSelLds = GTile<64, 256>::kStages * GTile<64, 256>::kStageBytes;
 static_assert(kSelLds >= 2 * 2 * kWrRows * 2 * kWrKC && GTile<64, 256>::kWaves == kWrWaves, "shared launch shape");
@@ -729,13 +749,15 @@ __global__ __launch_bounds__(64 * kWrWaves, 1) void grouped_gemm_sel_kernel(
     int E, float *__restrict__ out_f32, uint16_t *__restrict__ out_hi, uint16_t *__restrict__ out_lo,
     const uint8_t *__restrict__ tiled, uint64_t tiled_stride, uint64_t tiled_off) {
     __shared__ __align__(1024) uint8_t smem[kSelLds];
-    if (__builtin_amdgcn_readfirstlane(*choice))
+    const int plan = __builtin_amdgcn_readfirstlane(*choice), colmajor = plan >> 1;
+    if (plan & 1)
         gemm_wr_tile<MATS>(smem, blockIdx.x, experts, stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk,
-                           counts, offsets, m_off128, E, out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
+                           counts, offsets, m_off128, E, colmajor, out_f32, out_hi, out_lo, tiled, tiled_stride,
+                           tiled_off);
     else
         gemm_lds_tile<MATS, 64, 256>(smem, (uint32_t)(uintptr_t)smem, blockIdx.x, experts, stride, w_off, w3_off, N,
-                                     Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, E, out_f32, out_hi,
-                                     out_lo);
+                                     Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, E, colmajor,
+                                     out_f32, out_hi, out_lo);
 }
 
 // moe[t][d] = sum_k w[t][k] * y[pos_of[t*K+k]][d] in selection order (rabbit2.c:540); x += moe.
@@ -919,7 +941,7 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
                          (size_t)T * D * 2 + 2 * (size_t)D < (size_t)kWrBufRecords;
     const bool small = tile_rows == 32 || (tile_rows == 0 && P <= kSmallTileRowsPerExpert * E);
     const int mt_rows = small ? 32 : 64;
-    const int tall = !tall_ok || small ? 1 : (tile_rows == 128 ? 2 : (tile_rows == 64 ? 1 : 0));
+    const int tall = !tall_ok || small || tile_rows == 64 ? 1 : 2;
     const bool sel = !small && tall_ok;
     e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off,
                mt_rows, sel ? r.m_off128 : nullptr, r.choice, tall);
