@@ -84,10 +84,11 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *   "prefill_layout"      1 (default): the grouped GEMMs read the tiled expert copies made by
  *                         rbt_hip_prefill_layout, and rbt_hip_upload* makes them; 0: the blobs only.
  *   "prefill_tile_rows"   0 (default): the grouped GEMMs take tiles of 32 rows of an expert's list
- *                         while the experts average at most 16 rows, else 64 or 128 rows as the
- *                         device picks from the call's tokens-per-expert histogram; 32 / 64 / 128:
- *                         that tile height always (128 where the shape has it). Outputs agree within
- *                         the parity tolerance (the reduction runs in other chunks). */
+ *                         while the experts average at most 16 rows, else 128 rows where the shape
+ *                         has them (64 otherwise), in an order the device picks from the call's
+ *                         tokens-per-expert histogram; 32 / 64 / 128: that tile height always (128
+ *                         where the shape has it). Outputs agree within the parity tolerance (the
+ *                         reduction runs in other chunks). */
 int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
 
 /* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the
