@@ -75,6 +75,19 @@ def test_grouped_shapes(dev, grouped_from, shape):
         layer.close()
 
 
+@pytest.mark.parametrize("T", [2048, 2100])
+def test_grouped_pairs_past_dispatch_registers(dev, grouped_from, T):
+    """More than 16 x 64 x 4 = 4096 (token, slot) pairs: the dispatch keeps the first 4096 pairs' experts
+    and ranks in registers and carries the rest through pos_of; both halves must land in the lists."""
+    grouped_from(1)
+    layer = SynthLayer(dev, 256, 8, 2, 128, po.DT_BF16, 1, seed=11, w_scale=1.0, fan_in=True)
+    try:
+        xb = layer.make_x(T, seed=41)
+        check_grouped(dev, layer, xb, label=f"{T * 2} pairs")
+    finally:
+        layer.close()
+
+
 def test_grouped_matches_gemv_path(dev, grouped_from):
     """The same 24 tokens through the grouped path and the per-pair GEMV path: same routing and
     weights (the router is shared), outputs within the bar of each other and of the oracle."""
