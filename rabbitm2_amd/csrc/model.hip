@@ -436,14 +436,25 @@ __global__ __launch_bounds__(1024) void argmax_cand_kernel(const float2 *__restr
                                                            int32_t *__restrict__ seq, int ctx) {
     __shared__ float s_b[16];
     __shared__ int s_i[16];
+    // thread 0's step-state and first-logit loads go out with the candidates, not after the reduction
+    const float v0 = threadIdx.x == 0 ? logits[0] : 0.0f;
+    const int p = threadIdx.x == 0 ? st->pos : 0, n_prompt = threadIdx.x == 0 ? st->n_prompt : 0;
     float b = -INFINITY;
     int k = -1;
-    for (int q = threadIdx.x; q < nc; q += blockDim.x) {
-        const float2 c = cand[q];
-        const int ci = __float_as_int(c.y);
-        if (ci >= 0 && (k < 0 || c.x > b || (c.x == b && ci < k))) {
-            b = c.x;
-            k = ci;
+    // eight candidates per thread in flight at a time (indices clamped; a repeated candidate changes
+    // nothing: the comparison keeps the first of equal values and an equal index is not lower)
+    constexpr int kU = 8;
+    for (int q0 = threadIdx.x; q0 < nc; q0 += kU * blockDim.x) {
+        float2 c[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) c[u] = cand[min(q0 + u * (int)blockDim.x, nc - 1)];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int ci = __float_as_int(c[u].y);
+            if (ci >= 0 && (k < 0 || c[u].x > b || (c[u].x == b && ci < k))) {
+                b = c[u].x;
+                k = ci;
+            }
         }
     }
     for (int off = 32; off > 0; off >>= 1) {
@@ -468,11 +479,9 @@ __global__ __launch_bounds__(1024) void argmax_cand_kernel(const float2 *__restr
                 b = s_b[q];
                 k = s_i[q];
             }
-        const float v0 = logits[0];
         if (k < 0 || v0 != v0) k = 0;
-        const int p = st->pos;
         st->last = k;
-        if (p + 1 < ctx && p + 1 >= st->n_prompt) seq[p + 1] = k;
+        if (p + 1 < ctx && p + 1 >= n_prompt) seq[p + 1] = k;
         st->pos = p + 1;
     }
 }
