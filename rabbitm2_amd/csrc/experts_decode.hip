@@ -32,7 +32,7 @@ __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMI
 
 // XS > 0: the block also stages the token's activation row x (xu 16-byte units, at most XS per
 // thread, clamped loads and stores) into xs_lds; its loads are issued next to the logits load, so
-// they land while wave 0 ranks.
+// they land while wave 0 selects.
 template <int XS = 0>
 __device__ __forceinline__ void block_topk(const float *__restrict__ logits, int E, int K, int norm_topk, float *s_v, int *s_idx,
                            float *s_pw, float *s_w, const float *__restrict__ x = nullptr, f32x4 *xs_lds = nullptr,
@@ -69,30 +69,26 @@ __device__ __forceinline__ void block_topk(const float *__restrict__ logits, int
             sum = sum + v4.w;
         }
         const float p = e / sum;
-        wave_lds_sync();
-        s_v[lane] = p;
-        wave_lds_sync();
-        int rank;
         if (sum != sum) {
-            rank = lane;  // all NaN: the engine keeps the first unused index each round
-        } else {
-            // four independent counters keep the dependent-add chain short (entries past E are 0
-            // and never beat a probability of a real expert; lanes past E are not stored)
-            int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-#pragma unroll
-            for (int q = 0; q < EMAX_T / 4; ++q) {
-                const f32x4 v4 = p4[q];
-                const int j = 4 * q;
-                r0 += (v4.x > p) | ((v4.x == p) & (j < lane));
-                r1 += (v4.y > p) | ((v4.y == p) & (j + 1 < lane));
-                r2 += (v4.z > p) | ((v4.z == p) & (j + 2 < lane));
-                r3 += (v4.w > p) | ((v4.w == p) & (j + 3 < lane));
+            if (lane < K) {  // all NaN: the engine keeps the first unused index each round
+                s_idx[lane] = lane;
+                s_pw[lane] = p;
             }
-            rank = (r0 + r1) + (r2 + r3);
-        }
-        if (lane < E && rank < K) {
-            s_idx[rank] = lane;
-            s_pw[rank] = p;
+        } else {
+            // K rounds of the engine's selection: the largest remaining probability, the lowest index
+            // among equal ones (its strict '>' scan from index 0); a wave maximum and a ballot per
+            // round. Probabilities are finite and >= 0 here, so lanes past E (-1) never win and a
+            // taken lane (-2) is out for good.
+            float cand = lane < E ? p : -1.0f;
+            for (int k = 0; k < K; ++k) {
+                const float m = wave_max(cand);
+                const int w = __builtin_ctzll(__ballot(cand == m));
+                if (lane == w) {
+                    s_idx[k] = lane;
+                    s_pw[k] = p;
+                    cand = -2.0f;
+                }
+            }
         }
         wave_lds_sync();
         float wsum = 0.0f;

@@ -386,28 +386,25 @@ __device__ __forceinline__ void wave_softmax_topk(float v, int E, int K, int nor
         sum = sum + v4.w;
     }
     const float p = e / sum;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    s_v[lane] = p;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    int rank;
     if (sum != sum) {
-        rank = lane;  // all NaN: each round keeps the first unused index
-    } else {
-        int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const f32x4 v4 = p4[q];
-            const int j = 4 * q;
-            r0 += (v4.x > p) | ((v4.x == p) & (j < lane));
-            r1 += (v4.y > p) | ((v4.y == p) & (j + 1 < lane));
-            r2 += (v4.z > p) | ((v4.z == p) & (j + 2 < lane));
-            r3 += (v4.w > p) | ((v4.w == p) & (j + 3 < lane));
+        if (lane < K) {  // all NaN: each round keeps the first unused index
+            routing_t[lane] = lane;
+            s_p[lane] = p;
         }
-        rank = (r0 + r1) + (r2 + r3);
-    }
-    if (lane < E && rank < K) {
-        routing_t[rank] = lane;
-        s_p[rank] = p;
+    } else {
+        // K rounds of the selection: the largest remaining probability, the lowest index among equal
+        // ones; a wave maximum and a ballot per round. Probabilities are finite and >= 0 here, so
+        // lanes past E (-1) never win and a taken lane (-2) is out for good.
+        float cand = lane < E ? p : -1.0f;
+        for (int k = 0; k < K; ++k) {
+            const float m = wave_max(cand);
+            const int w = __builtin_ctzll(__ballot(cand == m));
+            if (lane == w) {
+                routing_t[k] = lane;
+                s_p[k] = p;
+                cand = -2.0f;
+            }
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float wsum = 0.0f;
