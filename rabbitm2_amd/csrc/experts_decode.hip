@@ -80,7 +80,7 @@ __device__ __forceinline__ void block_topk(const float *__restrict__ logits, int
             // round. Probabilities are finite and >= 0 here, so lanes past E (-1) never win and a
             // taken lane (-2) is out for good.
             float cand = lane < E ? p : -1.0f;
-            for (int k = 0; k < K; ++k) {
+            auto round = [&](int k) {
                 const float m = wave_max(cand);
                 const int w = __builtin_ctzll(__ballot(cand == m));
                 if (lane == w) {
@@ -88,6 +88,12 @@ __device__ __forceinline__ void block_topk(const float *__restrict__ logits, int
                     s_pw[k] = p;
                     cand = -2.0f;
                 }
+            };
+            if (K == 8) {  // the common top-8, unrolled
+#pragma unroll
+                for (int k = 0; k < 8; ++k) round(k);
+            } else {
+                for (int k = 0; k < K; ++k) round(k);
             }
         }
         wave_lds_sync();
