@@ -21,7 +21,8 @@ namespace rbt {
 namespace {
 
 constexpr int KMAX_T = 64;  // selected experts per token (the engine's MAX_TOPK, rabbit2.c:59)
-constexpr int kHStageMax = 16;  // 16-byte units of h per thread in the down kernel: K*H <= 16384 floats
+constexpr int kDownThreads = 512, kDownRows = 1;  // down kernel: block size, output rows per wave
+constexpr int kHStageMax = 8;  // 16-byte units of h per thread in the down kernel: K*H <= 16384 floats
 constexpr int EMAX_T = 64;  // experts per layer for the in-kernel top-k (one per lane of wave 0)
 
 // Softmax + top-k of one token's logits, the engine's arithmetic (rabbit2.c:399-405, :516-528,
@@ -225,10 +226,10 @@ __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restr
     }
 }
 
-// grid (ceil(D / (4*RW)), T), block 256, dynamic LDS K*H*4 bytes; requires H == NH * 64 * kPer.
-// HS: 16-byte units of h staged per thread (K*H/4 <= 256*HS).
-template <int DT, int NH, int RW, int HS>
-__global__ __launch_bounds__(256) void down_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
+// grid (ceil(D / (BT/64*RW)), T), block BT, dynamic LDS K*H*4 bytes; requires H == NH * 64 * kPer.
+// HS: 16-byte units of h staged per thread (K*H/4 <= BT*HS).
+template <int DT, int NH, int RW, int HS, int BT>
+__global__ __launch_bounds__(BT) void down_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
                                                         const int32_t *__restrict__ routing,
                                                         const float *__restrict__ weights,
                                                         const float *__restrict__ hbuf, int K, int D,
@@ -355,19 +356,19 @@ hipError_t gateup_nc(const Launch &L, const uint8_t *E, uint64_t stride, int32_t
 template <int DT, int NH>
 hipError_t down_nh(const Launch &L, const uint8_t *E, uint64_t stride, const int32_t *routing, const float *weights,
                    const float *hbuf, int T, int K, int D, float *x_inout, float *moe_out) {
-    constexpr int RW = 2;
+    constexpr int RW = kDownRows, BT = kDownThreads, WPB = BT / kWave;
     constexpr int H = NH * kWave * Elem<DT>::kPer;
-    const dim3 g((unsigned)((D + 4 * RW - 1) / (4 * RW)), (unsigned)T), b(256);
+    const dim3 g((unsigned)((D + WPB * RW - 1) / (WPB * RW)), (unsigned)T), b(BT);
     const uint32_t lds = (uint32_t)((size_t)K * H * 4);
-    const int per = (K * H / 4 + 255) / 256;  // h units per thread
+    const int per = (K * H / 4 + BT - 1) / BT;  // h units per thread
+    if (per <= 2)
+        return launch(L, down_fast_kernel<DT, NH, RW, 2, BT>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
+                      x_inout, moe_out);
     if (per <= 4)
-        return launch(L, down_fast_kernel<DT, NH, RW, 4>, g, b, lds, E, stride, routing, weights, hbuf, K, D, x_inout,
-                      moe_out);
-    if (per <= 8)
-        return launch(L, down_fast_kernel<DT, NH, RW, 8>, g, b, lds, E, stride, routing, weights, hbuf, K, D, x_inout,
-                      moe_out);
-    return launch(L, down_fast_kernel<DT, NH, RW, kHStageMax>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
-                  x_inout, moe_out);
+        return launch(L, down_fast_kernel<DT, NH, RW, 4, BT>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
+                      x_inout, moe_out);
+    return launch(L, down_fast_kernel<DT, NH, RW, kHStageMax, BT>, g, b, lds, E, stride, routing, weights, hbuf, K,
+                  D, x_inout, moe_out);
 }
 
 template <int DT>
@@ -404,7 +405,7 @@ bool experts_decode_supported(int dtype, int T, int K, int D, int H, const void 
     const int nc = D / step, nh = H / step;
     const bool nc_ok = D % step == 0 && (nc == 1 || nc == 2 || nc == 3 || nc == 4 || nc == 6 || nc == 8);
     const bool nh_ok = H % step == 0 && nh >= 1 && nh <= 4;
-    return nc_ok && nh_ok && H % 2 == 0 && T >= 1 && T <= 65535 && (size_t)K * H <= 4 * 256 * kHStageMax &&
+    return nc_ok && nh_ok && H % 2 == 0 && T >= 1 && T <= 65535 && (size_t)K * H <= 4 * (size_t)kDownThreads * kHStageMax &&
            aligned16(experts) && stride % 16 == 0 && aligned16(xb) && aligned16(hbuf);
 }
 
