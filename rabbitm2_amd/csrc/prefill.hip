@@ -55,9 +55,9 @@ constexpr int kDispRegs = 4;  // 64-pair steps per wave kept in registers by dis
 // Wave w owns the pair slice [w*S, (w+1)*S). A: each wave ranks its pairs, 64 at a time, against
 // equal experts (ballots over the expert-id bits) and keeps per-expert running counts in its own LDS
 // row; a pair's rank inside its wave's slice stays in a register (pos_of holds it past the first
-// kDispRegs steps). B: wave 0 (4 experts per lane) sums the waves' counts, scans them into the
-// offsets, and turns each wave's counts into that wave's first position per expert. C: every pair
-// adds its wave's base. Three barriers in all.
+// kDispRegs steps). B: every thread (wave w, expert e) sums the counts of the waves before w, wave 0
+// (4 experts per lane) scans the totals into the offsets, and every thread turns its sum into wave
+// w's first position for e. C: every pair adds its wave's base. Five barriers in all.
 __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restrict__ routing, int P, int E,
                                                         int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                                         int32_t *__restrict__ perm, int32_t *__restrict__ pos_of,
@@ -66,6 +66,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                                                         int tall) {
     constexpr int NW = 16;
     __shared__ int s_w[NW][kDispatchMaxE];  // A: running counts per wave; B: each wave's base positions
+    __shared__ int s_tot[kDispatchMaxE];    // B: each expert's total, then its first list position
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int S = ((P + NW - 1) / NW + 63) / 64 * 64;  // slice per wave, whole 64-pair steps
     const int base = wv * S, end = min(P, base + S);
@@ -106,14 +107,26 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
         if (valid) pos_of[p] = rk;
     }
     __syncthreads();
+    // B1: thread (wave w, lane l) sums the counts of waves before w for experts l + 64 j (all threads,
+    // instead of one wave walking the 16 waves per expert); wave 15 also keeps the totals
+    int pre[kDispatchMaxE / 64];
+#pragma unroll
+    for (int j = 0; j < kDispatchMaxE / 64; ++j) {
+        const int e = lane + 64 * j;
+        int run = 0;
+        if (e < E) {
+            for (int w = 0; w < wv; ++w) run += s_w[w][e];
+            if (wv == NW - 1) s_tot[e] = run + s_w[NW - 1][e];
+        }
+        pre[j] = run;
+    }
+    __syncthreads();
     if (wv == 0) {
         int c[4], mt[4], mt2[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = 4 * lane + i;
-            int tot = 0;
-            if (e < E)
-                for (int w = 0; w < NW; ++w) tot += s_w[w][e];
+            const int tot = e < E ? s_tot[e] : 0;
             c[i] = tot;
             mt[i] = (tot + mt_rows - 1) / mt_rows;
             mt2[i] = (tot + 127) / 128;
@@ -146,12 +159,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
                 offsets[e] = oc;
                 m_off[e] = om;
                 if (m_off2) m_off2[e] = om2;
-                int run = oc;  // each wave's first position for expert e
-                for (int w = 0; w < NW; ++w) {
-                    const int n = s_w[w][e];
-                    s_w[w][e] = run;
-                    run += n;
-                }
+                s_tot[e] = oc;  // the expert's first list position
             }
             if (e == E - 1) {
                 offsets[E] = oc + c[i];
@@ -165,6 +173,13 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(const int32_t *__restric
             om += mt[i];
             om2 += mt2[i];
         }
+    }
+    __syncthreads();
+    // B3: each wave's first position for each expert
+#pragma unroll
+    for (int j = 0; j < kDispatchMaxE / 64; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E) s_w[wv][e] = s_tot[e] + pre[j];
     }
     __syncthreads();
 #pragma unroll
