@@ -711,8 +711,10 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
         dev.profile(0)
         counts = dev.expert_counts(E)
         # the GEMMs' row tiles, by the device's rule: 32 rows while the experts average at most 16, else
-        # 128 rows, their slots column-major where some list is longer than 4x the mean
+        # 128 rows (512 weight rows wide at this shape), their slots column-major where some list is
+        # longer than 4x the mean
         tile_rows = 32 if P <= 16 * E else 128
+        tile_weight_rows = 512 if tile_rows == 128 and H % 256 == 0 and D % 512 == 0 else 256
         tiles = int(sum((c + tile_rows - 1) // tile_rows for c in counts))
         slot_order = "column-major" if tile_rows == 128 and int(counts.max()) * E > 4 * P else "expert-major"
         issued_rows = int(sum((c + 15) // 16 * 16 for c in counts))
@@ -736,6 +738,7 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             "kernels": kern,
             "tokens_per_expert": [int(c) for c in counts],
             "tile_rows": tile_rows,
+            "tile_weight_rows": tile_weight_rows,
             "row_tiles": tiles,
             "slot_order": slot_order,
         }

@@ -88,7 +88,11 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *                         has them (64 otherwise), in an order the device picks from the call's
  *                         tokens-per-expert histogram; 32 / 64 / 128: that tile height always (128
  *                         where the shape has it). Outputs agree within the parity tolerance (the
- *                         reduction runs in other chunks). */
+ *                         reduction runs in other chunks).
+ *   "prefill_wide"        1 (default): 128-row tiles span 512 weight rows (gate/up: 256 W1 + 256 W3
+ *                         rows; H a multiple of 256, D of 512), so each activation row fetched
+ *                         serves twice the weight bytes; 0: 256 weight rows. Outputs agree within
+ *                         rounding (the k-chunks run in another rotated order). */
 int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
 
 /* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the

@@ -130,6 +130,7 @@ struct rbt_hip {
     uint64_t seed = 0;
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
     int prefill_tile_rows = 0;  // option "prefill_tile_rows": rows per grouped-GEMM tile, 0 = by batch
+    bool prefill_wide = true;   // option "prefill_wide": 128-row tiles 512 weight rows wide
     const int32_t *expert_counts = nullptr;  // histogram of the last grouped-path call
     // staging for the host-pointer entry points: device buffer and its pinned host twin
     void *stage = nullptr;
@@ -596,7 +597,8 @@ int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float 
     HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown),
                              next_nw ? no_combine : lc(h, kProfCombine), L->experts, L->expert_stride, xb, T,
                              L->n_experts, L->top_k, L->dim, L->expert_hidden, routing, w.weights, w.hbuf, w.pre, x,
-                             nullptr, &counts, true, next_nw == nullptr, h->prefill_tile_rows, tiled_for(h, L)));
+                             nullptr, &counts, true, next_nw == nullptr, h->prefill_tile_rows, tiled_for(h, L),
+                             h->prefill_wide));
     h->expert_counts = counts;
     if (next_nw) {  // the combine, fused with the RMSNorm the next step starts with (xb and its planes)
         const float *y = nullptr;
@@ -890,7 +892,7 @@ int moe_block(rbt_hip *h, const rbt_moe_layer *L, const float *xb_dev, int T, fl
         HIP_OK(h, launch_prefill(lc(h, kProfDispatch), lc(h, kProfGateup), lc(h, kProfDown), lc(h, kProfCombine),
                                  L->experts, L->expert_stride, xb_dev, T, L->n_experts, L->top_k, L->dim,
                                  L->expert_hidden, routing, weights, w.hbuf, w.pre, x_dev, moe_dev, &counts, fused,
-                                 true, h->prefill_tile_rows, tiled_for(h, L)));
+                                 true, h->prefill_tile_rows, tiled_for(h, L), h->prefill_wide));
         h->expert_counts = counts;
         return done();
     }
@@ -1385,6 +1387,8 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
         if (value != 0 && value != 32 && value != 64 && value != 128)
             return fail(h, "set_option: prefill_tile_rows must be 0, 32, 64 or 128");
         h->prefill_tile_rows = (int)value;
+    } else if (strcmp(name, "prefill_wide") == 0) {
+        h->prefill_wide = value != 0;
     } else {
         return fail(h, "set_option: unknown option '%s'", name);
     }

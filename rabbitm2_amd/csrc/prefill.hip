@@ -775,6 +775,217 @@ __global__ __launch_bounds__(64 * kWrWaves, 1) void grouped_gemm_sel_kernel(
                                      out_f32, out_hi, out_lo);
 }
 
+// ---------------------------------------------------------------- grouped GEMM, wide 128-row tiles
+// The 128-row tile twice as wide: 512 weight rows (gate/up: 256 W1 rows and the same 256 W3 rows; down:
+// 512 W2 rows), so each activation row read from L2 serves twice the weight bytes. A CU moves its
+// bytes at a bounded rate whatever their source, and the 256-row tile reads as many activation bytes
+// as weight bytes, so this halves the activation share of the traffic. Eight waves of 256 registers:
+// wave W owns weight rows 64 W .. 64 W + 63 as four 16-row column groups (gate/up: W1 for W < 4, W3 for
+// W >= 4); accumulators [8 row groups][4 column groups]; weights one 64-wide k-step ahead in
+// registers, activations two k-steps ahead in registers and one ahead in a two-stage LDS ring. Same
+// operands and products per output element as gemm_wr_tile (k-chunks of 64, each as two 32-wide
+// halves, hi then lo); the chunks are rotated per wide tile, so sums agree within rounding.
+constexpr int kWdWaves = 8, kWdGroups = 4;
+constexpr bool gemm_wide_supported(int mats, int N, int Kd) {
+    return N % (mats == 2 ? 256 : 512) == 0 && Kd % (2 * kWrKC) == 0;
+}
+template <int MATS>
+__global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
+    const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
+    const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
+    int topk, const int32_t *__restrict__ counts, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ m_off, const int32_t *__restrict__ choice, int E, float *__restrict__ out_f32,
+    uint16_t *__restrict__ out_hi, uint16_t *__restrict__ out_lo, const uint8_t *__restrict__ tiled,
+    uint64_t tiled_stride, uint64_t tiled_off) {
+    constexpr int NT = 64 * kWdWaves;              // threads
+    constexpr int NTILE = MATS == 2 ? 256 : 512;   // output columns per tile
+    constexpr int RG = kWrRows / 16;               // row groups of 16
+    constexpr int ROWB = 2 * kWrKC;                // bytes of an activation row per k-step
+    constexpr int ABYTES = kWrRows * ROWB;         // one plane of a k-step, 16 KiB
+    constexpr int AU = 2 * ABYTES / 16 / NT;       // 16-byte activation units per thread per k-step (4)
+    constexpr int XBYTES = (kWdWaves / 2) * RG * kWdGroups * 64 * 16;  // gate/up epilogue exchange, 128 KiB
+    constexpr int LDSB = MATS == 2 ? XBYTES : 2 * 2 * ABYTES;
+    static_assert(AU * NT * 16 == 2 * ABYTES && LDSB >= 2 * 2 * ABYTES, "ring sizes");
+    __shared__ __align__(1024) uint8_t smem[LDSB];
+    uint8_t(*ring)[2 * ABYTES] = reinterpret_cast<uint8_t(*)[2 * ABYTES]>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, W = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int colmajor = (__builtin_amdgcn_readfirstlane(*choice) >> 1) & 1;
+    const unsigned bid = blockIdx.x;
+    const int ntiles_n = N / NTILE;
+    const int total = m_off[E] * ntiles_n;
+    const int range = (total + 7) >> 3;
+    const int slot = (int)(bid >> 3);
+    const int tau = (int)(bid & 7) * range + slot;
+    if (slot >= range || tau >= total) return;
+    int e, jt, il;
+    tile_of(tau, m_off, E, ntiles_n, colmajor, &e, &jt, &il);
+    const int row0 = offsets[e] + il * kWrRows;
+    const int rows = __builtin_amdgcn_readfirstlane(min(kWrRows, counts[e] - il * kWrRows));
+    const int n0 = jt * NTILE;
+    const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
+    const int nch = Kd / kWrKC;
+    // step c reads k-chunk (c + rot) mod nch, rot a function of the weight tile and the same for the
+    // whole block (every wave stages the step's activation chunk for all of them)
+    const int rot = (e * ntiles_n + jt) % nch;
+    auto cidx = [&](int c) { return c + rot < nch ? c + rot : c + rot - nch; };
+    const int jn = 2 * jt + (MATS == 2 ? ((W & 3) >> 1) : (W >> 2));  // the 256-row tile of this wave's rows
+
+    // weight operands of this lane, column group g: tile row 64 W + 16 g + (lane & 15), k offset
+    // 8 * (lane >> 4) in each 32-wide half s of a 64-wide k-chunk cc, at wp + g * wg + cc * wck + s * wsb
+    const uint8_t *wp;
+    size_t wck, wsb, wg;
+    if (tiled) {
+        // row block of the 256-row tile jn (tiled copy order, see prefill_layout_kernel)
+        const int wn = MATS == 2 ? (W >= 4 ? 8 : 0) + 4 * (W & 1) : 4 * (W & 3);
+        wp = tiled + (size_t)e * tiled_stride + tiled_off + (size_t)jn * nch * kTiledChunk + (size_t)(2 * wn) * 1024 +
+             16 * lane;
+        wck = kTiledChunk;
+        wsb = 1024;
+        wg = 2048;
+    } else {
+        const uint8_t *base = experts + (size_t)e * stride + (MATS == 2 && W >= 4 ? w3_off : w_off);
+        const int wr = n0 + (MATS == 2 ? 64 * (W & 3) : 64 * W) + (lane & 15);
+        wp = base + (size_t)wr * rowb + 16 * (lane >> 4);
+        wck = ROWB;
+        wsb = 64;
+        wg = 16 * rowb;
+    }
+    const size_t base_row = gather ? 0 : (size_t)row0;
+    const __amdgpu_buffer_rsrc_t rs[2] = {
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a_hi) + base_row * Kd, 0, kWrBufRecords, kBufConfig),
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(a_lo) + base_row * Kd, 0, kWrBufRecords, kBufConfig)};
+    uint32_t aoff[AU], adst[AU];
+#pragma unroll
+    for (int i = 0; i < AU; ++i) {
+        const int u = tid + NT * i, pl = u / (ABYTES / 16), r = (u % (ABYTES / 16)) / (ROWB / 16), g = u % (ROWB / 16);
+        const int lr = row0 + (r < rows ? r : 0);
+        const size_t arow = gather ? (size_t)(perm[lr] / topk) : (size_t)lr;
+        aoff[i] = r < rows ? (uint32_t)((arow - base_row) * rowb + 16 * g) : (uint32_t)kWrBufRecords;
+        adst[i] = (uint32_t)(pl * ABYTES + r * ROWB + 16 * (g ^ ((r >> 1) & 7)));
+    }
+    static_assert(2 * (ABYTES / 16) == AU * NT && (ABYTES / 16) % NT == 0, "unit i's plane is i / (AU / 2)");
+    u32x4 aset[2][AU];
+    u32x4 wv[2][kWdGroups][2];  // [slot][column group][32-wide half]
+    auto load_a = [&](u32x4 (&dst)[AU], int c) {
+        const uint32_t kb = (uint32_t)(cidx(c) * ROWB);
+#pragma unroll
+        for (int i = 0; i < AU; ++i)
+            dst[i] = __builtin_amdgcn_raw_buffer_load_b128(rs[i / (AU / 2)], (int)(aoff[i] + kb), 0, 0);
+    };
+    auto store_a = [&](const u32x4 (&src)[AU], int buf) {
+#pragma unroll
+        for (int i = 0; i < AU; ++i) *reinterpret_cast<u32x4 *>(&ring[buf][adst[i]]) = src[i];
+    };
+    auto load_w = [&](u32x4 (&dst)[kWdGroups][2], int c) {
+        const size_t kb = (size_t)cidx(c) * wck;
+#pragma unroll
+        for (int g = 0; g < kWdGroups; ++g)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) dst[g][s2] = ld_stream_u4(wp + g * wg + kb + s2 * wsb);
+    };
+
+    f32x4 acc[RG][kWdGroups];
+#pragma unroll
+    for (int q = 0; q < RG; ++q)
+#pragma unroll
+        for (int g = 0; g < kWdGroups; ++g) acc[q][g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // k-step c on slot J = c % 2; LAST: the tile's final two steps (nch is even). Each step stores the
+    // next step's activations, issues activations (two steps ahead) before weights (one step ahead),
+    // so the store waits for activations issued a step earlier, never for the weights in flight.
+    auto step = [&](auto jc, auto lastc, int c) {
+        constexpr int J = decltype(jc)::value;
+        constexpr bool LAST = decltype(lastc)::value;
+        if constexpr (!LAST || J == 0) store_a(aset[J ^ 1], (c + 1) & 1);
+        if constexpr (!LAST) load_a(aset[J], c + 2);
+        if constexpr (!LAST || J == 0) load_w(wv[J ^ 1], c + 1);
+        const uint8_t *st = ring[c & 1];
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            if (16 * q < rows) {  // wave-uniform: the row group holds list entries
+                const int r = 16 * q + (lane & 15);
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const int g8 = 4 * s2 + (lane >> 4);
+                    const int off = r * ROWB + 16 * (g8 ^ ((r >> 1) & 7));
+                    const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + off));
+                    const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(st + ABYTES + off));
+#pragma unroll
+                    for (int g = 0; g < kWdGroups; ++g) {
+                        const bf16x8 bv = __builtin_bit_cast(bf16x8, wv[J][g][s2]);
+                        acc[q][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, acc[q][g], 0, 0, 0);
+                        acc[q][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, acc[q][g], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // prologue, in the steady state's order: activations of steps 0 and 1, weights of step 0
+    load_a(aset[0], 0);
+    load_w(wv[0], 0);
+    load_a(aset[1], 1);
+    store_a(aset[0], 0);
+    __syncthreads();
+    int c0 = 0;
+    for (; c0 + 2 < nch; c0 += 2) {
+        step(I0{}, std::false_type{}, c0);
+        step(I1{}, std::false_type{}, c0 + 1);
+    }
+    step(I0{}, std::true_type{}, c0);
+    step(I1{}, std::true_type{}, c0 + 1);
+
+    // epilogue: acc[q][g] lane holds tile row 64 W + 16 g + (lane % 16) for list rows 16 q + 4 (lane / 16) + i
+    if constexpr (MATS == 2) {
+        f32x4 *xch = reinterpret_cast<f32x4 *>(smem);  // [W - 4][q][g][lane]
+        if (W >= kWdWaves / 2) {
+#pragma unroll
+            for (int q = 0; q < RG; ++q)
+                if (16 * q < rows)
+#pragma unroll
+                    for (int g = 0; g < kWdGroups; ++g)
+                        xch[(((W - kWdWaves / 2) * RG + q) * kWdGroups + g) * 64 + lane] = acc[q][g];
+        }
+        __syncthreads();
+        if (W >= kWdWaves / 2) return;
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            if (16 * q >= rows) break;
+#pragma unroll
+            for (int g = 0; g < kWdGroups; ++g) {
+                const f32x4 up = xch[((W * RG + q) * kWdGroups + g) * 64 + lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * q + 4 * (lane >> 4) + i;
+                    if (r >= rows) continue;
+                    const float gg = acc[q][g][i], u = up[i];
+                    const float v = (gg / (1.0f + expf(-gg))) * u;  // silu(g) * u, rabbit2.c:535-537
+                    const uint32_t hb = f32_to_bf16_rne(v);
+                    const uint32_t lb = f32_to_bf16_rne(v - __uint_as_float(hb << 16));
+                    const size_t o = (size_t)(row0 + r) * N + n0 + 64 * W + 16 * g + (lane & 15);
+                    out_hi[o] = (uint16_t)hb;
+                    out_lo[o] = (uint16_t)lb;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < RG; ++q) {
+            if (16 * q >= rows) break;
+#pragma unroll
+            for (int g = 0; g < kWdGroups; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * q + 4 * (lane >> 4) + i;
+                    if (r >= rows) continue;
+                    out_f32[(size_t)(row0 + r) * N + n0 + 64 * W + 16 * g + (lane & 15)] = acc[q][g][i];
+                }
+        }
+    }
+}
+
 // moe[t][d] = sum_k w[t][k] * y[pos_of[t*K+k]][d] in selection order (rabbit2.c:540); x += moe.
 __global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restrict__ y,
                                                           const int32_t *__restrict__ pos_of,
@@ -844,6 +1055,21 @@ hipError_t launch_gemm_sel(const Launch &L, const uint8_t *experts, uint64_t str
     return launch(L, grouped_gemm_sel_kernel<MATS>, dim3((unsigned)blocks), dim3(64 * kWrWaves), 0, experts, stride,
                   w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, m_off128, choice, E,
                   out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
+}
+
+template <int MATS>
+hipError_t launch_gemm_wide(const Launch &L, const uint8_t *experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
+                            int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
+                            int topk, const int32_t *counts, const int32_t *offsets, const int32_t *m_off128,
+                            const int32_t *choice, int E, int max_mtiles, float *out_f32, uint16_t *out_hi,
+                            uint16_t *out_lo, const uint8_t *tiled, uint64_t tiled_stride, uint64_t tiled_off) {
+    if (!gemm_wide_supported(MATS, N, Kd)) return hipErrorInvalidValue;
+    const long long tiles = (long long)max_mtiles * (N / (MATS == 2 ? 256 : 512));  // >= the 128-row tiles
+    const long long blocks = (tiles + 7) / 8 * 8;
+    if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
+    return launch(L, grouped_gemm_wide_kernel<MATS>, dim3((unsigned)blocks), dim3(64 * kWdWaves), 0, experts, stride,
+                  w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off128, choice, E, out_f32,
+                  out_hi, out_lo, tiled, tiled_stride, tiled_off);
 }
 
 }  // namespace
@@ -923,7 +1149,8 @@ void prefill_x_planes(void *ws, int T, int E, int K, int D, uint16_t **x_hi, uin
 hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, const Launch &Lc, const void *experts,
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
-                          int32_t **counts_out, bool x_split_done, bool combine, int tile_rows, const void *tiled) {
+                          int32_t **counts_out, bool x_split_done, bool combine, int tile_rows, const void *tiled,
+                          bool wide_ok) {
     if (tile_rows != 0 && tile_rows != 32 && tile_rows != 64 && tile_rows != 128) return hipErrorInvalidValue;
     if (T <= 0 || K <= 0) return hipErrorInvalidValue;  // the dispatch reads at least one pair
     const int P = T * K;
@@ -961,6 +1188,8 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
     e = launch(Ldd, dispatch_kernel, dim3(1), dim3(1024), 0, routing, P, E, counts, offsets, perm, pos_of, m_off,
                mt_rows, sel ? r.m_off128 : nullptr, r.choice, tall);
     if (e != hipSuccess) return e;
+    // 128-row tiles (the dispatch picks them whenever tall == 2) in the wide kernel where the shape has it
+    const bool wide = sel && tall == 2 && wide_ok && gemm_wide_supported(2, H, D) && gemm_wide_supported(1, D, H);
     const uint8_t *ex = static_cast<const uint8_t *>(experts);
     const int max_mtiles = (P + mt_rows - 1) / mt_rows + E;  // >= sum over experts of ceil(count / mt_rows)
     const uint64_t w3 = (uint64_t)H * D * 2, w2 = 2 * (uint64_t)H * D * 2;
@@ -973,6 +1202,9 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
     else if (!sel)
         e = launch_gemm<2, 64, 256>(Lg, ex, stride, 0, w3, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, E,
                                     max_mtiles, nullptr, h_hi, h_lo);
+    else if (wide)
+        e = launch_gemm_wide<2>(Lg, ex, stride, 0, w3, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, r.m_off128,
+                                r.choice, E, max_mtiles, nullptr, h_hi, h_lo, tl, tstride, 0);
     else
         e = launch_gemm_sel<2>(Lg, ex, stride, 0, w3, H, D, x_hi, x_lo, 1, perm, K, counts, offsets, m_off, r.m_off128,
                                r.choice, E, max_mtiles, nullptr, h_hi, h_lo, tl, tstride, 0);
@@ -984,6 +1216,9 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
     else if (!sel)
         e = launch_gemm<1, 64, 256>(Lw, ex, stride, w2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets, m_off, E,
                                     max_mtiles, y, nullptr, nullptr);
+    else if (wide)
+        e = launch_gemm_wide<1>(Lw, ex, stride, w2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets, r.m_off128,
+                                r.choice, E, max_mtiles, y, nullptr, nullptr, tl, tstride, w2);
     else
         e = launch_gemm_sel<1>(Lw, ex, stride, w2, 0, D, H, h_hi, h_lo, 0, perm, K, counts, offsets, m_off, r.m_off128,
                                r.choice, E, max_mtiles, y, nullptr, nullptr, tl, tstride, w2);

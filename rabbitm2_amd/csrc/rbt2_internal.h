@@ -162,7 +162,7 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
                           uint64_t stride, const float *xb, int T, int E, int K, int D, int H, const int32_t *routing,
                           const float *weights, float *hbuf, void *ws, float *x_inout, float *moe_out,
                           int32_t **counts_out, bool x_split_done,
-                          bool combine = true, int tile_rows = 0, const void *tiled = nullptr);
+                          bool combine = true, int tile_rows = 0, const void *tiled = nullptr, bool wide_ok = true);
 // The tiled copy of a layer's bf16 experts that the 128-row grouped GEMMs stream contiguously (same
 // bytes as the blobs, in tile order): whether the shape has one, its size, and the re-layout launch
 // (experts in the blob layout with stride, into dst). tiled = that copy, or nullptr for the blobs.
