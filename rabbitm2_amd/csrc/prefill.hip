@@ -16,10 +16,12 @@
 //    instead of 8. A full 64-row tile then does 64 rows x 2 parts x 2 flop = 256 flop per weight
 //    element, 128 flop per weight byte: below the bf16 MFMA/HBM ridge (2.5 PFLOP/s / 8 TB/s =
 //    312), so the kernels stay bound by HBM.
-//    Tiles: 128 or 64 rows x 256 weight rows per block of 16 waves (or 32 x 128 per 8 waves for
-//    decode-sized batches); the reduction runs in chunks of 32, 64 (128) through a four- or three-stage
-//    LDS ring filled by direct HBM -> LDS copies (weights and activations). 128-row tiles cover the
-//    whole list of an expert with up to 128 rows, so its weight tile is streamed by one block once.
+//    Tiles: 128 rows x 512 weight rows per block of 8 waves (grouped_gemm_wide_kernel, where the
+//    shape has them), 128 or 64 rows x 256 weight rows per block of 16 waves, or 32 x 128 per 8 waves
+//    for decode-sized batches; the 64- and 32-row tiles run the reduction in chunks of 64 (128)
+//    through a three- or four-stage LDS ring filled by direct HBM -> LDS copies, the 128-row tiles
+//    keep their weight operands in registers. 128-row tiles cover the whole list of an expert with
+//    up to 128 rows, so its weight tile is streamed by one block once.
 //    Tile order (expert, column tile, row tile), split into 8 contiguous ranges, one per XCD (the
 //    hardware hands block b to XCD b % 8): the row tiles of a hot expert then share each weight
 //    tile in that XCD's L2, and an expert's activation rows are reused across its column tiles.
