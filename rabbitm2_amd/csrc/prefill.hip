@@ -805,7 +805,7 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
     constexpr int ROWB = 2 * kWrKC;                // bytes of an activation row per k-step
     constexpr int ABYTES = kWrRows * ROWB;         // one plane of a k-step, 16 KiB
     constexpr int AU = 2 * ABYTES / 16 / NT;       // 16-byte activation units per thread per k-step (4)
-    constexpr int XBYTES = (kWdWaves / 2) * RG * kWdGroups * 64 * 16;  // gate/up epilogue exchange, 128 KiB
+    constexpr int XBYTES = kWdWaves * (RG / 2) * kWdGroups * 64 * 16;  // gate/up epilogue exchange, 128 KiB
     constexpr int LDSB = MATS == 2 ? XBYTES : 2 * 2 * ABYTES;
     static_assert(AU * NT * 16 == 2 * ABYTES && LDSB >= 2 * 2 * ABYTES, "ring sizes");
     __shared__ __align__(1024) uint8_t smem[LDSB];
@@ -941,37 +941,58 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
 
     // epilogue: acc[q][g] lane holds tile row 64 W + 16 g + (lane % 16) for list rows 16 q + 4 (lane / 16) + i
     if constexpr (MATS == 2) {
-        f32x4 *xch = reinterpret_cast<f32x4 *>(smem);  // [W - 4][q][g][lane]
-        if (W >= kWdWaves / 2) {
+        // waves W and W + 4 hold the gate (W1) and up (W3) sums of the same columns; each computes the
+        // SwiGLU of half the row groups (W: 0-3, W + 4: 4-7) and hands the partner the other half
+        // through LDS, so all eight waves share the exp / divide work
+        constexpr int HQ = RG / 2;
+        f32x4 *xch = reinterpret_cast<f32x4 *>(smem);  // [wave][HQ][group][lane]
+        const bool upw = W >= kWdWaves / 2;  // wave-uniform: each branch below indexes acc by constants
+        const int partner = upw ? W - kWdWaves / 2 : W + kWdWaves / 2;
+        auto send = [&](auto qc) {
+            constexpr int QS = decltype(qc)::value;
 #pragma unroll
-            for (int q = 0; q < RG; ++q)
-                if (16 * q < rows)
+            for (int qq = 0; qq < HQ; ++qq)
+                if (16 * (QS + qq) < rows)
 #pragma unroll
                     for (int g = 0; g < kWdGroups; ++g)
-                        xch[(((W - kWdWaves / 2) * RG + q) * kWdGroups + g) * 64 + lane] = acc[q][g];
-        }
-        __syncthreads();
-        if (W >= kWdWaves / 2) return;
+                        xch[((W * HQ + qq) * kWdGroups + g) * 64 + lane] = acc[QS + qq][g];
+        };
+        auto finish = [&](auto qc, auto upc) {
+            constexpr int QM = decltype(qc)::value;
+            constexpr bool UP = decltype(upc)::value;
 #pragma unroll
-        for (int q = 0; q < RG; ++q) {
-            if (16 * q >= rows) break;
+            for (int qq = 0; qq < HQ; ++qq) {
+                const int q = QM + qq;
+                if (16 * q >= rows) break;
 #pragma unroll
-            for (int g = 0; g < kWdGroups; ++g) {
-                const f32x4 up = xch[((W * RG + q) * kWdGroups + g) * 64 + lane];
+                for (int g = 0; g < kWdGroups; ++g) {
+                    const f32x4 other = xch[((partner * HQ + qq) * kWdGroups + g) * 64 + lane];
+                    const f32x4 gv = UP ? other : acc[q][g], uv = UP ? acc[q][g] : other;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * q + 4 * (lane >> 4) + i;
-                    if (r >= rows) continue;
-                    const float gg = acc[q][g][i], u = up[i];
-                    const float v = (gg / (1.0f + expf(-gg))) * u;  // silu(g) * u, rabbit2.c:535-537
-                    const uint32_t hb = f32_to_bf16_rne(v);
-                    const uint32_t lb = f32_to_bf16_rne(v - __uint_as_float(hb << 16));
-                    const size_t o = (size_t)(row0 + r) * N + n0 + 64 * W + 16 * g + (lane & 15);
-                    out_hi[o] = (uint16_t)hb;
-                    out_lo[o] = (uint16_t)lb;
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = 16 * q + 4 * (lane >> 4) + i;
+                        if (r >= rows) continue;
+                        const float gg = gv[i], u = uv[i];
+                        const float v = (gg / (1.0f + expf(-gg))) * u;  // silu(g) * u, rabbit2.c:535-537
+                        const uint32_t hb = f32_to_bf16_rne(v);
+                        const uint32_t lb = f32_to_bf16_rne(v - __uint_as_float(hb << 16));
+                        const size_t o = (size_t)(row0 + r) * N + n0 + 64 * (W & 3) + 16 * g + (lane & 15);
+                        out_hi[o] = (uint16_t)hb;
+                        out_lo[o] = (uint16_t)lb;
+                    }
                 }
             }
-        }
+        };
+        using IH = std::integral_constant<int, HQ>;
+        if (upw)
+            send(I0{});
+        else
+            send(IH{});
+        __syncthreads();
+        if (upw)
+            finish(IH{}, std::true_type{});
+        else
+            finish(I0{}, std::false_type{});
     } else {
 #pragma unroll
         for (int q = 0; q < RG; ++q) {
