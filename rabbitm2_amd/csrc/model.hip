@@ -342,22 +342,25 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // through LDS. Lane l of a 16 x 16 result holds rows 4 (l / 16) + v, token l % 16.
 // MODE 0: segment outputs; 1: resid[b][r] += (one segment). SPLIT: the block takes the one token block
 // blockIdx.y (TB = 1) -- for products with few row tiles, so that twice the blocks share the chip and
-// each reads half the planes.
+// each reads half the planes. RT: row tiles of 16 per block (segments whole multiples of 16 RT rows),
+// each wave's activation operands serving all of them, so the planes are read once per 16 RT weight
+// rows; every row tile runs the same MFMA sequence and slice order as with RT = 1 (bit-identical).
 template <int KS>
 struct MfmaShape {
     static constexpr int NW = KS >= 4 ? 16 : 4 * KS;  // waves per block
     static constexpr int WS = 4 * KS / NW;             // k-steps per wave (1..4)
 };
-template <int KS, int TB, int MODE, bool SPLIT = false>
+template <int KS, int TB, int MODE, bool SPLIT = false, int RT = 1>
 __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__restrict__ x_hi,
                                                           const uint16_t *__restrict__ x_lo, int B, Segs sg,
                                                           int total_rows, float *__restrict__ resid) {
     constexpr int K = 128 * KS, NW = MfmaShape<KS>::NW, WS = MfmaShape<KS>::WS;
     static_assert(WS >= 1 && WS <= 4 && NW * WS * 32 == K, "k split");
     static_assert(!SPLIT || TB == 1, "one token block per block");
-    __shared__ f32x4 part[NW][TB][kWave];
+    static_assert(RT == 1 || (MODE == 0 && !SPLIT), "several row tiles: segment outputs only");
+    __shared__ f32x4 part[NW][RT][TB][kWave];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row0 = blockIdx.x * 16;
+    const int row0 = blockIdx.x * 16 * RT;
     const int tbase = SPLIT ? (int)blockIdx.y : 0;  // this block's first token block
     const int tbt = (B + 15) / 16;                   // token blocks of the planes
     int s = 0, r = row0;  // the tile's segment and first row in it (segments are whole tiles)
@@ -367,12 +370,16 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
     }
     const size_t koff = (size_t)w * WS * 32 + 8 * (lane >> 4);
     const uint8_t *wp = sg.W[s] + ((size_t)(r + (lane & 15)) * K + koff) * 2;
-    u32x4 a[WS];
+    u32x4 a[RT][WS];
 #pragma unroll
-    for (int i = 0; i < WS; ++i) a[i] = ld_stream_u4(wp + 64 * i);
-    f32x4 acc[TB];
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < WS; ++i) a[rt][i] = ld_stream_u4(wp + (size_t)rt * 16 * K * 2 + 64 * i);
+    f32x4 acc[RT][TB];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) acc[rt][tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int tb0 = 0; tb0 < TB; tb0 += 2) {
         constexpr int NBMAX = TB < 2 ? TB : 2;
@@ -393,32 +400,38 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < WS; ++i) {
-            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a[i]);
 #pragma unroll
-            for (int j = 0; j < NBMAX; ++j) {
-                if (tb0 + j < TB) {
-                    acc[tb0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        av, __builtin_bit_cast(bf16x8_t, bh[i][j]), acc[tb0 + j], 0, 0, 0);
-                    acc[tb0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        av, __builtin_bit_cast(bf16x8_t, bl[i][j]), acc[tb0 + j], 0, 0, 0);
+            for (int rt = 0; rt < RT; ++rt) {
+                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a[rt][i]);
+#pragma unroll
+                for (int j = 0; j < NBMAX; ++j) {
+                    if (tb0 + j < TB) {
+                        acc[rt][tb0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            av, __builtin_bit_cast(bf16x8_t, bh[i][j]), acc[rt][tb0 + j], 0, 0, 0);
+                        acc[rt][tb0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            av, __builtin_bit_cast(bf16x8_t, bl[i][j]), acc[rt][tb0 + j], 0, 0, 0);
+                    }
                 }
             }
         }
     }
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) part[w][tb][lane] = acc[tb];
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) part[w][rt][tb][lane] = acc[rt][tb];
     __syncthreads();
-    // one output element per thread: (block tb, lane l, element j) summed over the NW slices in order
+    // one output element per thread: (row tile rt, block tb, lane l, element j) summed over the NW
+    // slices in order
     const float *pf = reinterpret_cast<const float *>(part);
-    for (int e = threadIdx.x; e < TB * kWave * 4; e += blockDim.x) {
+    for (int e = threadIdx.x; e < RT * TB * kWave * 4; e += blockDim.x) {
         float v[NW];
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww) v[ww] = pf[(size_t)ww * TB * kWave * 4 + e];
+        for (int ww = 0; ww < NW; ++ww) v[ww] = pf[(size_t)ww * RT * TB * kWave * 4 + e];
         float sum = v[0];
 #pragma unroll
         for (int ww = 1; ww < NW; ++ww) sum = sum + v[ww];
-        const int tb = e / (kWave * 4), l = (e / 4) % kWave, j = e % 4;
-        const int t = 16 * (tbase + tb) + (l & 15), rr = 4 * (l >> 4) + j;
+        const int rt = e / (TB * kWave * 4), tb = (e / (kWave * 4)) % TB, l = (e / 4) % kWave, j = e % 4;
+        const int t = 16 * (tbase + tb) + (l & 15), rr = 16 * rt + 4 * (l >> 4) + j;
         if (t >= B) continue;
         if constexpr (MODE == 1) {
             float *dst = resid + (size_t)t * total_rows + row0 + rr;
@@ -1358,6 +1371,15 @@ hipError_t dense_mfma_ks(const Launch &L, const uint16_t *xh, const uint16_t *xl
     if (tbt >= 2 && total / 16 < kMfmaSplitTiles)  // few row tiles: a block per (row tile, token block)
         return launch(L, dense_mfma_kernel<KS, 1, MODE, true>, dim3((unsigned)(total / 16), (unsigned)tbt), b, 0, xh, xl,
                       B, sg, total, resid);
+    // two row tiles per block where every segment is whole 32-row pairs (the planes read once per 32
+    // weight rows)
+    if constexpr (MODE == 0) {
+        if (tbt <= 2 && sg.rows[0] % 32 == 0 && sg.rows[1] % 32 == 0 && sg.rows[2] % 32 == 0) {
+            const dim3 g2((unsigned)(total / 32));
+            return tbt == 1 ? launch(L, dense_mfma_kernel<KS, 1, 0, false, 2>, g2, b, 0, xh, xl, B, sg, total, resid)
+                            : launch(L, dense_mfma_kernel<KS, 2, 0, false, 2>, g2, b, 0, xh, xl, B, sg, total, resid);
+        }
+    }
     switch (tbt) {
         case 1: return launch(L, dense_mfma_kernel<KS, 1, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
         case 2: return launch(L, dense_mfma_kernel<KS, 2, MODE>, g, b, 0, xh, xl, B, sg, total, resid);
