@@ -575,7 +575,7 @@ int model_alloc(rbt_hip *h, const ModelLayout &m) {
 // otherwise only pos advances. Everything is enqueued on the handle stream, nothing waits, so a step
 // can be captured into a graph.
 // The MoE block of the batched forward for 2..kRouterDecodeMaxT tokens on the grouped expert path: the
-// RMSNorm and the router logits in one launch (router_decode_kernel<M, true>, 16 x T blocks: xb and
+// RMSNorm and the router logits in one launch (router_decode_kernel<M, true>, E / 2 or E / 4 x T blocks: xb and
 // the logits), top-k + the activation split, then dispatch, the grouped GEMMs and the combine into x
 // (rabbit2.c:512-542 for each token).
 int moe_grouped_norm(rbt_hip *h, const rbt_moe_layer *L, const float *nw, float eps, int T, float *x, float *xb,

@@ -185,8 +185,11 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 
 }
 
-// Few tokens (decode), AVX2 order, bf16 weights, D a multiple of 128: one 64-thread block per 4 router
-// rows of one token, thread (row rr, chain c). Chain c's operands are staged transposed in LDS --
+// Few tokens (decode), AVX2 order, bf16 weights, D a multiple of 128: one 64-thread block per DR router
+// rows of one token, thread (row rr, chain c). DR = 2 while the blocks fit the CUs once (each block
+// stages x plus fewer weight bytes before its chains start; one OLMoE MoE layer 24.4 against 24.7 us
+// with 4 rows), lanes 32-63 then staging only; DR = 4 for more tokens (at 32 tokens 5.5 against
+// 7.2 us: every block stages its token's x). Chain c's operands are staged transposed in LDS --
 // wt[rr][c][m] = W[r][16m + c], xt[c][m] = x[16m + c] -- so a 16-byte read carries 8 steps of one
 // chain (48 reads for 128 steps instead of 256 narrow ones) and the chain's dependent adds are the
 // only long pole. Staging: a thread takes 8 consecutive steps of 8 chains (eight 16-byte loads of
@@ -196,8 +199,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 // NORM: the kernel also runs the RMSNorm in front of the router (rabbit2.c:512): x is the residual
 // stream, xb = x * inv * nw with inv = 1/sqrtf(sum x^2 / D + eps) from the block's own staging loads,
 // and block (0, t) writes token t's xb to xb_out for the expert kernels.
-constexpr int kDRows = 4;
-template <int M, bool NORM = false>  // steps per chain = D / 16, a multiple of 8
+template <int M, bool NORM = false, int DR = 4>  // steps per chain = D / 16, a multiple of 8
 __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restrict__ xb, const uint16_t *__restrict__ W,
                                                           const float *__restrict__ bias, int E,
                                                           float *__restrict__ logits, const float *__restrict__ nw = nullptr,
@@ -206,6 +208,8 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
     constexpr int WP = M + 8;  // bf16 per (row, chain) line: 16-byte pad, lanes of one read hit distinct banks
     constexpr int XP = M + 4;  // f32 per chain line
     constexpr int G = M / 8;   // 8-step groups per chain
+    constexpr int kDRows = DR;
+    static_assert(DR == 2 || DR == 4, "rows per block");
     __shared__ __align__(16) uint16_t wt[kDRows * 16 * WP];
     __shared__ __align__(16) float xt[16 * XP];
     const int tid = threadIdx.x, rr = tid >> 4, c = tid & 15;
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
     __syncthreads();
 
     // ---- chain c of row rr, 128 steps in column order (rounded product, then add)
-    const uint16_t *wl = &wt[(rr * 16 + c) * WP];
+    const uint16_t *wl = &wt[(min(rr, kDRows - 1) * 16 + c) * WP];  // lanes past the rows: clamped, no write
     const float *xl = &xt[c * XP];
     float acc = 0.0f;
 #pragma unroll 4
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
 #pragma unroll
     for (int R = 1; R < kDRows; ++R) sum = rr == R ? rs[R] : sum;
     const int r = r0 + rr;
-    if (c == 0 && r < E) {
+    if (c == 0 && rr < kDRows && r < E) {
         if (bias) sum = sum + bias[r];
         logits[(size_t)t * E + r] = sum;
     }
@@ -415,7 +419,7 @@ __device__ __forceinline__ void wave_softmax_topk(float v, int E, int K, int nor
 // Softmax + top-k of token t's E <= 64 logits (wave 0 of block t, the engine's arithmetic as above) and
 // the bf16 hi/lo split of its activation row (every thread, 8 elements per 16-byte pair): the grouped
 // expert path's front end for a few tokens whose logits and normalised rows router_decode_kernel<M,
-// true> has just written (16 x T blocks for the chains instead of the fused prefill kernel's one
+// true> has just written (E / 2 or E / 4 x T blocks for the chains instead of the fused prefill kernel's one
 // block per two tokens).
 __global__ __launch_bounds__(256) void topk_split_kernel(const float *__restrict__ logits, int E, int K, int norm_topk,
                                                          const float *__restrict__ xb, int D,
@@ -865,15 +869,18 @@ inline bool decode_ok(int T, int D, int dtype, const void *W, const float *xb) {
            (reinterpret_cast<uintptr_t>(xb) % 16 == 0);
 }
 
+constexpr int kRouterTwoRowBlocks = 256;  // blocks up to which the decode router takes 2 rows per block
 template <bool NORM>
 inline hipError_t launch_router_decode_t(const Launch &L, const float *xb, const void *W, const float *bias, int T,
                                          int E, int D, float *logits, const float *nw, float eps, float *xb_out) {
-    const dim3 g((unsigned)((E + kDRows - 1) / kDRows), (unsigned)T), b(64);
+    const bool two = (long long)((E + 1) / 2) * T <= kRouterTwoRowBlocks;  // rows per block, see the kernel
+    const dim3 g((unsigned)(two ? (E + 1) / 2 : (E + 3) / 4), (unsigned)T), b(64);
     const uint16_t *w = static_cast<const uint16_t *>(W);
     switch (D / 16) {
-#define RD_CASE(m) \
-    case m:        \
-        return launch(L, router_decode_kernel<m, NORM>, g, b, 0, xb, w, bias, E, logits, nw, eps, xb_out);
+#define RD_CASE(m)                                                                                                \
+    case m:                                                                                                       \
+        return two ? launch(L, router_decode_kernel<m, NORM, 2>, g, b, 0, xb, w, bias, E, logits, nw, eps, xb_out) \
+                   : launch(L, router_decode_kernel<m, NORM, 4>, g, b, 0, xb, w, bias, E, logits, nw, eps, xb_out);
         RD_CASE(8)
         RD_CASE(16)
         RD_CASE(32)
