@@ -107,7 +107,7 @@ hipError_t launch_router(const Launch &L, const Launch &Lk, int order, int dtype
                          const float *bias, int T, int E, int D, int K, int norm_topk, float *probs,
                          int32_t *routing, float *weights);
 
-// Tokens up to which the AVX2-order router logits run on the decode kernel (16 x T blocks of 64
+// Tokens up to which the AVX2-order router logits run on the decode kernel (E / 4 x T blocks of 64
 // threads; at 32 tokens 5.0 us against 19.9 us for the batch kernel, and with the top-k + split launch
 // 9.7 us against 18.1 us for the fused prefill front end; at 512 tokens 28.2 + 4.7 against 19.5 us).
 constexpr int kRouterDecodeMaxT = 64;
