@@ -239,25 +239,30 @@ def test_tiled_expert_copy_is_bitwise_the_blobs(dev, grouped_from, tile_rows, bi
         layer.close()
 
 
-@pytest.mark.parametrize("biased", [False, True], ids=["uniform", "skewed"])
-def test_wide_tiles_agree_with_256_row_tiles(dev, grouped_from, biased):
-    """The OLMoE layer at 512 tokens on 128-row tiles 512 weight rows wide (the default where the shape
-    has them) and 256 wide (option prefill_wide = 0): both held to the oracle, and within rounding of
-    each other (the same products, summed in k-chunks rotated per tile)."""
+@pytest.mark.parametrize("biased,T", [(False, 512), (True, 512), (False, 1024)],
+                         ids=["uniform", "skewed", "uniform-1024"])
+def test_wide_tiles_agree_with_256_row_tiles(dev, grouped_from, biased, T):
+    """The OLMoE layer on 128-row tiles 512 weight rows wide (the default where the shape has them) and
+    256 wide (option prefill_wide = 0): both held to the oracle, and within rounding of each other (the
+    same products, summed in k-chunks rotated per tile). 512 tokens: one row tile per expert (uniform,
+    expert-major slots) or three for the hot experts (skewed, column-major); 1024 evenly routed tokens:
+    ~128 rows per expert, so experts span two row tiles in expert-major order."""
     grouped_from(1)
     bias = np.zeros(64, np.float32)
     if biased:
         bias[:8] = 2.0
     layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=4, bias=bias)
     try:
-        xb = layer.make_x(512, seed=6)
-        x = layer.make_x(512, seed=16, bf16=False)
+        xb = layer.make_x(T, seed=6)
+        x = layer.make_x(T, seed=16, bf16=False)
         dev.set_option("prefill_wide", 0)
         narrow, _ = check_grouped(dev, layer, xb, x=x, label="256 weight rows")
         dev.set_option("prefill_wide", 1)
         wide, _ = check_grouped(dev, layer, xb, x=x, label="512 weight rows")
         assert np.array_equal(wide["routing"], narrow["routing"])
         assert normwise_err(wide["moe"], narrow["moe"]) <= 1e-5
+        if T == 1024:
+            assert int((dev.expert_counts(64) > 128).sum()) > 0  # some lists span two row tiles
     finally:
         dev.set_option("prefill_wide", 1)
         layer.close()
