@@ -1048,6 +1048,48 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const float *__restri
     if (x_inout) x_inout[o] = xo + moe;
 }
 
+// combine_rows_kernel for K <= 8 with four columns per thread (D % 4 == 0, 16-byte aligned rows): the
+// same arithmetic per element, a quarter of the load instructions, every y row load of the thread in
+// flight before the sums.
+__global__ __launch_bounds__(256) void combine_rows4_kernel(const float *__restrict__ y,
+                                                           const int32_t *__restrict__ pos_of,
+                                                           const float *__restrict__ weights, int K, int D,
+                                                           float *__restrict__ x_inout, float *__restrict__ moe_out) {
+    const int t = blockIdx.y;
+    const int d = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (d >= D) return;
+    const size_t o = (size_t)t * D + d;
+    int p[8];
+    float wk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int kc = min(k, K - 1);
+        p[k] = pos_of[t * K + kc];
+        wk[k] = weights[t * K + kc];
+    }
+    const f32x4 xo = x_inout ? *reinterpret_cast<const f32x4 *>(x_inout + o) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 tmp[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tmp[k] = *reinterpret_cast<const f32x4 *>(y + (size_t)p[k] * D + d);
+    f32x4 moe = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+#pragma clang fp contract(off)
+        if (k < K) {
+            moe.x = moe.x + wk[k] * tmp[k].x;
+            moe.y = moe.y + wk[k] * tmp[k].y;
+            moe.z = moe.z + wk[k] * tmp[k].z;
+            moe.w = moe.w + wk[k] * tmp[k].w;
+        }
+    }
+    if (moe_out) *reinterpret_cast<f32x4 *>(moe_out + o) = moe;
+    if (x_inout) {
+#pragma clang fp contract(off)
+        const f32x4 xn = f32x4{xo.x + moe.x, xo.y + moe.y, xo.z + moe.z, xo.w + moe.w};
+        *reinterpret_cast<f32x4 *>(x_inout + o) = xn;
+    }
+}
+
 template <int MATS, int ROWS, int WROWS>
 hipError_t launch_gemm(const Launch &L, const uint8_t *experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
                        int N, int Kd, const uint16_t *a_hi, const uint16_t *a_lo, int gather, const int32_t *perm,
@@ -1247,6 +1289,10 @@ hipError_t launch_prefill(const Launch &Ld, const Launch &Lg, const Launch &Lw, 
                                r.choice, E, max_mtiles, y, nullptr, nullptr, tl, tstride, w2);
     if (e != hipSuccess) return e;
     if (!combine) return hipSuccess;
+    const auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    if (K <= 8 && D % 4 == 0 && a16(y) && (!x_inout || a16(x_inout)) && (!moe_out || a16(moe_out)))
+        return launch(Lc, combine_rows4_kernel, dim3((unsigned)((D / 4 + 255) / 256), (unsigned)T), dim3(256), 0,
+                      (const float *)y, (const int32_t *)pos_of, weights, K, D, x_inout, moe_out);
     return launch(Lc, combine_rows_kernel, dim3((unsigned)((D + 255) / 256), (unsigned)T), dim3(256), 0,
                   (const float *)y, (const int32_t *)pos_of, weights, K, D, x_inout, moe_out);
 }
