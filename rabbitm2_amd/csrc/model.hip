@@ -528,8 +528,8 @@ __device__ __forceinline__ void attn_load_round(float (&kr)[kAttnKG][AE], float 
 #pragma unroll
         for (int e = 0; e < AE; ++e) {
             const int i = lane + kWave * e;
-            kr[g][e] = i < hd ? kt[i] : 0.0f;
-            vr[g][e] = i < hd ? vt[i] : 0.0f;
+            kr[g][e] = i < hd ? __builtin_nontemporal_load(kt + i) : 0.0f;
+            vr[g][e] = i < hd ? __builtin_nontemporal_load(vt + i) : 0.0f;
         }
     }
 }
@@ -554,8 +554,8 @@ __device__ __forceinline__ void attn_g8_load(f32x4 (&kr)[4], f32x4 (&vr)[4], con
     const size_t o = (size_t)t * kv_dim + (size_t)kvh * kAttnG8Hd + 4 * j;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        kr[i] = *reinterpret_cast<const f32x4 *>(kc + o + 32 * i);
-        vr[i] = *reinterpret_cast<const f32x4 *>(vc + o + 32 * i);
+        kr[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(kc + o + 32 * i));
+        vr[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(vc + o + 32 * i));
     }
 }
 

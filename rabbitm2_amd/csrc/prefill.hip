@@ -234,6 +234,10 @@ __global__ __launch_bounds__(256) void split_hilo_kernel(const float *__restrict
 __device__ __forceinline__ void lds_dma16(const void *g, uint32_t lds_byte) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_byte), "v"(g) : "memory", "m0");
 }
+// The same for data read once (expert weights): a streaming (non-temporal) load.
+__device__ __forceinline__ void lds_dma16_stream(const void *g, uint32_t lds_byte) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds_byte), "v"(g) : "memory", "m0");
+}
 template <int N>
 __device__ __forceinline__ void wait_dma() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -413,7 +417,7 @@ __device__ __forceinline__ void gemm_lds_tile(
         const size_t kb = (size_t)cc * ROWB;
 #pragma unroll
         for (int i = 0; i < WI; ++i)
-            lds_dma16(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (WI * w + i) * 1024));
+            lds_dma16_stream(wsrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + (WI * w + i) * 1024));
 #pragma unroll
         for (int i = 0; i < AI; ++i)
             if (aon[i]) lds_dma16(asrc[i] + kb, __builtin_amdgcn_readfirstlane(sb + WBYTES + (AI * w + i) * 1024));
