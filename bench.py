@@ -7,14 +7,16 @@ layers, hidden 2048, 16 heads x 128 with QK-norm and RoPE, 64 experts top-8, Swi
 bf16 weights ~N(0, 0.02), f32 KV cache in HBM -- on a 128-token random prompt, through the device-side
 --gen loop (one HIP graph replay per token, the argmax on the device feeding the next step). One step =
 one token's forward() + final norm + lm_head + argmax. W untimed steps, then a fresh run of the prompt
-and K + 1 generated tokens whose K steps after the first are timed with HIP events on the library's
-stream (default K = 255: the 256 generated tokens of the workload). value = K / their time.
+and the workload's 256 generated tokens (K + 1 if K > 255), whose last K steps are timed with HIP
+events on the library's stream (default K = 255: every step after the first token). value = K / their
+time.
 
 The same JSON line carries:
   roofline  the dominant kernel of that step (the MoE gate/up kernel: softmax + top-k, the 8 selected
             experts' w1/w3 rows, SwiGLU): algorithmic bytes / its average duration, from HIP events
-            around every launch in eager forward() steps at the generated positions; traffic from the
-            calibrated rocprofv3 counter runs kept under profiles/.
+            around every launch in eager forward() steps at the timed positions; traffic from the
+            calibrated rocprofv3 counter runs kept under profiles/. --profile-forward 383 runs the same
+            eager steps for a kernel trace and prints the same event timings beside it.
   layer     the MoE layer alone (the metric's "MoE-layer HBM GB/s & % of peak"): 16 OLMoE-shaped MoE
             layers with renormalised top-8, one token per step, each layer reading its own 100.9 MB,
             replayed from a HIP graph; per-layer time, HBM rate, per-kernel times; the host-pointer
@@ -48,7 +50,6 @@ TRAFFIC_KEY = {"gateup": "gateup_fast"}
 KERNEL_DESC = {"gateup": "gateup_fast (softmax + top-k, expert gate+up projections, SwiGLU)"}
 STEP_KERNELS = ("embed", "qkv", "attention", "attn_merge", "wo", "router", "gateup", "down_combine", "lm_head",
                 "argmax")
-PROFILE_STEPS = 32  # eager forward() steps timed per kernel after the timed run
 
 
 def hip_events():
@@ -150,6 +151,11 @@ def main():
 
     from rabbitm2_amd import hip as rh
 
+    if rh.profiler_attached() and not args.copy_calib_mib:
+        print("bench.py: a profiler tool is attached to this process, and the bench's legs replay HIP graphs, "
+              "which are off under a profiler (traced replays have crashed the host process). Trace the eager "
+              "modes instead: --profile-forward N, --profile-decode N, --profile-prefill N.", file=sys.stderr)
+        sys.exit(2)
     dev = rh.Device(0)
     hipapi, mk, elapsed = hip_events()
     if args.copy_calib_mib:
@@ -171,40 +177,35 @@ def main():
     # ---- headline: whole-model bs=1 greedy decode
     cfg, setup_s = make_full_model(dev)
     dev.set_router_order(rh.ORDER_AVX2)
+    # every run decodes the workload's whole 256 tokens (more if K asks for more) and times the last K
+    # steps of it; generated step g forwards token g - 1 at position N_PROMPT + g - 1
     K_steps = args.steps
-    n_gen = K_steps + 1
-    ctx = N_PROMPT + max(n_gen, args.warmup + 1, PROFILE_STEPS + 1)
+    n_gen = max(N_GEN, K_steps + 1)
+    first_timed = n_gen - K_steps
+    pos_first, pos_last = N_PROMPT + first_timed - 1, N_PROMPT + n_gen - 2
+    ctx = N_PROMPT + max(n_gen, args.warmup + 1)
     dev.state_init(ctx)
     prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, N_PROMPT).astype(np.int32)
     warm = []
     if args.warmup > 0:
         warm, _ = dev.generate(prompt, args.warmup + 1)  # graph capture and first touch; untimed
+    dev.set_option("generate_timed_from", first_timed)
     w0 = time.perf_counter()
-    ids, (p_ms, g_ms) = dev.generate(prompt, n_gen)  # K timed steps: the forwards after the first token
+    ids, (p_ms, g_ms) = dev.generate(prompt, n_gen)  # g_ms: the last K steps
     wall = time.perf_counter() - w0
+    dev.set_option("generate_timed_from", 1)
     assert len(ids) == n_gen and all(0 <= t < cfg.vocab for t in ids)
     assert ids[:len(warm)] == warm, "generate is not deterministic"
     ms_per_step = g_ms / K_steps
     value = K_steps / (g_ms * 1e-3)
-    mean_pos = N_PROMPT + (n_gen - 1) / 2.0
-    tok_bytes = step_bytes(cfg, mean_pos)
+    tok_bytes = np.mean([step_bytes(cfg, p) for p in range(pos_first, pos_last + 1)])
 
-    # ---- per-kernel durations of the step: HIP events around every launch (deferred profiling, nothing
-    # waits between launches) in eager forward() steps at the generated positions
-    dev.state_init(ctx)
-    seq = prompt.tolist() + ids  # the timed run's tokens, padded with random ids for short runs
-    seq += np.random.default_rng(SEED + 1).integers(0, cfg.vocab, max(0, N_PROMPT + PROFILE_STEPS - len(seq))).tolist()
-    for pos in range(N_PROMPT):
-        dev.forward(seq[pos], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
-    dev.profile(2)
-    for pos in range(N_PROMPT, N_PROMPT + PROFILE_STEPS):
-        dev.forward(seq[pos], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
-    kern = {}
-    for name in STEP_KERNELS:
-        tot, n = dev.profile_get(name)
-        if n:
-            kern[name] = {"avg_us": round(1000.0 * tot / n, 3), "launches_per_step": n // PROFILE_STEPS}
-    dev.profile(0)
+    # ---- per-kernel durations of the step: HIP events around every launch (deferred profiling: no wait
+    # between launches inside a step) in eager forward() steps at the timed positions, over the KV cache
+    # the timed run left (each re-run writes its position's K/V row again with the same values)
+    seq = prompt.tolist() + ids
+    prof_pos = profile_positions(pos_first, pos_last)
+    kern = eager_step_kernels(dev, cfg, seq, prof_pos)
     esz = 2
     alg = {"gateup": K * 2 * H * D * esz + D * 4 + K * H * 4,  # the 8 experts' w1/w3 rows, x, h written
            "down_combine": K * D * H * esz + K * H * 4 + D * 4,
@@ -238,14 +239,17 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "OLMoE-1B-7B-shaped random-init model, batch-1 greedy decode: 16 layers, hidden 2048, 16 "
-                        "heads x 128 (QK-norm, RoPE), 64 experts top-8, SwiGLU 1024, vocab 50304, bf16 weights "
-                        "~N(0,0.02), f32 KV cache in HBM; 128-token random prompt, then 256 generated tokens "
-                        "(255 timed steps), one HIP graph replay per token",
+            "workload": f"OLMoE-1B-7B-shaped random-init model, batch-1 greedy decode: {cfg.n_layers} layers, hidden "
+                        f"{cfg.dim}, {cfg.n_heads} heads x {cfg.head_dim} (QK-norm, RoPE), {cfg.n_experts} experts "
+                        f"top-{cfg.top_k}, SwiGLU {cfg.expert_hidden}, vocab {cfg.vocab}, bf16 weights ~N(0,0.02), "
+                        f"f32 KV cache in HBM; {N_PROMPT}-token random prompt, then {len(ids)} generated tokens, "
+                        f"the last {K_steps} steps timed (positions {pos_first}..{pos_last}), one HIP graph replay "
+                        "per token",
             "model": "OLMoE-1B-7B shape", "layers": cfg.n_layers, "dim": cfg.dim, "n_experts": cfg.n_experts,
             "top_k": cfg.top_k, "expert_hidden": cfg.expert_hidden, "vocab": cfg.vocab, "weights": "bf16",
             "activations": "f32", "router_order": "avx2 (bit-exact engine order)", "global_batch": 1,
-            "prompt_tokens": N_PROMPT, "generated_tokens": n_gen,
+            "prompt_tokens": N_PROMPT, "generated_tokens": len(ids), "timed_steps": K_steps,
+            "timed_positions": [pos_first, pos_last],
         },
         "roofline": {
             "bound": "hbm",
@@ -258,7 +262,11 @@ def main():
             "traffic_source": "profiles/olmoe_moe_layer_traffic.json" if traffic else None,
             "alg_bytes_per_launch": alg["gateup"],
             "avg_launch_us": dom["avg_us"],
-            "timing": f"HIP events around each launch, {PROFILE_STEPS} eager decode steps x 16 layers",
+            "timing": f"HIP events around each launch in eager forward() steps at {len(prof_pos)} of the timed "
+                      f"positions ({prof_pos[0]}..{prof_pos[-1]}) x {cfg.n_layers} layers",
+            "launches": dom["launches"],
+            "trace_check": "profiles/olmoe_forward_decode_kernels.md: rocprofv3 kernel trace and these HIP "
+                           "events of the same eager steps in one process (bench.py --profile-forward)",
         },
         "full_model": {
             "bytes_per_token": int(tok_bytes),
@@ -282,6 +290,34 @@ def main():
         out["layer"] = moe_layer_leg(dev, args)
     print(json.dumps(out), flush=True)
     dev.close()
+
+
+PROFILE_MAX_STEPS = 255  # eager steps timed per kernel (the library keeps 4096 event pairs per kernel)
+
+
+def profile_positions(pos_first, pos_last):
+    """At most PROFILE_MAX_STEPS positions spread evenly over [pos_first, pos_last], in order."""
+    n = pos_last - pos_first + 1
+    if n <= PROFILE_MAX_STEPS:
+        return list(range(pos_first, pos_last + 1))
+    return sorted({pos_first + (i * (n - 1)) // (PROFILE_MAX_STEPS - 1) for i in range(PROFILE_MAX_STEPS)})
+
+
+def eager_step_kernels(dev, cfg, seq, positions):
+    """Per-kernel durations from HIP events around every launch (profiling mode 2) in eager forward()
+    steps of token seq[p] at each position p; the KV cache must already hold the positions before
+    each p. Returns {kernel: {avg_us, launches, launches_per_step}}."""
+    dev.profile(2)
+    for pos in positions:
+        dev.forward(seq[pos], pos, cfg.vocab, cfg.n_layers, cfg.top_k)
+    kern = {}
+    for name in STEP_KERNELS:
+        tot, n = dev.profile_get(name)
+        if n:
+            kern[name] = {"avg_us": round(1000.0 * tot / n, 3), "launches": int(n),
+                          "launches_per_step": n // len(positions)}
+    dev.profile(0)
+    return kern
 
 
 def host_pointer_moe(dev, cfg, reps=200):
@@ -464,9 +500,12 @@ def make_full_model(dev):
 
 def profile_forward(steps, batch):
     """`steps` eager forward steps of the whole model over random ids, for kernel traces (no HIP graphs,
-    no bench line). batch 0: rbt_hip_forward at positions 0 .. steps-1; batch B > 0: rbt_hip_forward_batch
-    of B sequences at positions B_CTX .. B_CTX + steps - 1 of the batched leg's context (the caches
-    below hold the zeros of batch_init instead of a filled context; the kernels read the same bytes)."""
+    no bench line). batch 0: rbt_hip_forward at positions 0 .. steps-1, the positions from N_PROMPT on
+    also timed per kernel with HIP events as the bench times them (printed as one JSON line on stderr,
+    so a trace of this run and the bench's event timing can be compared launch for launch); 383 steps
+    are the bench's prompt and its 255 timed positions. batch B > 0: rbt_hip_forward_batch of B
+    sequences at positions B_CTX .. B_CTX + steps - 1 of the batched leg's context (the caches below
+    hold the zeros of batch_init instead of a filled context; the kernels read the same bytes)."""
     from rabbitm2_amd import hip as rh
     dev = rh.Device(0)
     cfg, _ = make_full_model(dev)
@@ -475,9 +514,15 @@ def profile_forward(steps, batch):
     t0 = time.perf_counter()
     if batch <= 0:
         dev.state_init(max(steps, 1))
-        prompt = rng.integers(0, cfg.vocab, steps).astype(np.int32)
-        for p in range(steps):
-            dev.forward(int(prompt[p]), p, cfg.vocab, cfg.n_layers, cfg.top_k)
+        seq = rng.integers(0, cfg.vocab, steps).astype(np.int32).tolist()
+        n_pre = min(N_PROMPT, steps)
+        for p in range(n_pre):
+            dev.forward(seq[p], p, cfg.vocab, cfg.n_layers, cfg.top_k)
+        if steps > n_pre:
+            timed = list(range(n_pre, steps))
+            kern = eager_step_kernels(dev, cfg, seq, timed)
+            print(json.dumps({"profile_forward_events": kern, "positions": [timed[0], timed[-1]]}), file=sys.stderr,
+                  flush=True)
     else:
         dev.batch_init(batch, B_CTX + steps)
         for p in range(steps):
@@ -659,9 +704,34 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
     alg_bytes = E * 3 * H * D * esz + E * D * esz + T * D * 2 + T * D * 4
     alg_flops = T * 2 * E * D + P * 6 * H * D
     gemm_flops = {"gateup": P * 4 * H * D, "down_combine": P * 2 * H * D}
-    # the grouped GEMMs read the tiled copy of the experts made here where they take 128-row tiles
     layer0 = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride)
-    dev.prefill_layout(layer0)
+    res = {}
+    # first the experts as the converter stores them (the .rbt2 blobs, the default), then with the
+    # opt-in tiled copy (rbt_hip_prefill_layout) that the 128-row grouped GEMMs read where it exists
+    for layout_name in ("blobs", "tiled_copy"):
+        if layout_name == "tiled_copy":
+            dev.prefill_layout(layer0)
+        res[layout_name] = prefill_workloads(dev, routers, experts, stride, xb, moe, bias_dev, reps, alg_bytes,
+                                             alg_flops, gemm_flops)
+    dev.prefill_layout_drop(layer0)
+    out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,
+           "expert_layout": "uniform / skewed: the experts read in the .rbt2 storage format (the default); tiled_copy: "
+                            "the same calls with the opt-in tiled copy of layer 0 (rbt_hip_prefill_layout)",
+           "note": f"per-call time of the whole MoE block (router .. combine), HIP graph of {PREFILL_GRAPH_CALLS} "
+                   "calls replayed (us_per_call_eager: back-to-back eager calls), inputs in HBM",
+           **res["blobs"], "tiled_copy": res["tiled_copy"]}
+    if with_cpu:
+        out["cpu_baseline"] = cpu_prefill(dev, routers, experts, stride, xs, 64)
+    for b in (xb, moe, bias_dev):
+        dev.free(b)
+    return out
+
+
+def prefill_workloads(dev, routers, experts, stride, xb, moe, bias_dev, reps, alg_bytes, alg_flops, gemm_flops):
+    """The 512-token call with uniform and with skewed routing (+2.0 on experts 0-7): graph-replayed and
+    eager per-call times, per-kernel event times, histogram, HBM rate and matrix-core use."""
+    from rabbitm2_amd import hip as rh
+    T, P, esz = PREFILL_T, PREFILL_T * K, 2
     res = {}
     for name, bias in (("uniform", None), ("skewed", bias_dev)):
         L = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride, bias)  # layer 0
@@ -742,17 +812,7 @@ def prefill_leg(dev, routers, experts, stride, reps, with_cpu):
             "row_tiles": tiles,
             "slot_order": slot_order,
         }
-    dev.prefill_layout_drop(layer0)
-    out = {"tokens": T, "alg_bytes": alg_bytes, "alg_flops": alg_flops,
-           "expert_layout": "128-row tiles read the tiled copy (rbt_hip_prefill_layout), 64-row tiles the blobs",
-           "note": f"per-call time of the whole MoE block (router .. combine), HIP graph of {PREFILL_GRAPH_CALLS} "
-                   "calls replayed (us_per_call_eager: back-to-back eager calls), inputs in HBM",
-           **res}
-    if with_cpu:
-        out["cpu_baseline"] = cpu_prefill(dev, routers, experts, stride, xs, 64)
-    for b in (xb, moe, bias_dev):
-        dev.free(b)
-    return out
+    return res
 
 
 def cpu_prefill(dev, routers, experts, stride, xs, n):

@@ -81,8 +81,9 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *                         expert FFN run as grouped GEMMs on the matrix cores, each expert's weights
  *                         read once per call. Smaller T runs one GEMV per pair. Routing is the same
  *                         either way; outputs agree within the parity tolerance.
- *   "prefill_layout"      1 (default): the grouped GEMMs read the tiled expert copies made by
- *                         rbt_hip_prefill_layout, and rbt_hip_upload* makes them; 0: the blobs only.
+ *   "prefill_layout"      1 (default): the grouped GEMMs read a layer's tiled expert copy where the
+ *                         caller made one with rbt_hip_prefill_layout (none exists otherwise: by
+ *                         default every kernel reads the .rbt2 blobs); 0: the blobs only.
  *   "prefill_tile_rows"   0 (default): the grouped GEMMs take tiles of 32 rows of an expert's list
  *                         while the experts average at most 16 rows, else 128 rows where the shape
  *                         has them (64 otherwise), in an order the device picks from the call's
@@ -92,7 +93,10 @@ int rbt_hip_set_router_order(rbt_hip *h, int order);
  *   "prefill_wide"        1 (default): 128-row tiles span 512 weight rows (gate/up: 256 W1 + 256 W3
  *                         rows; H a multiple of 256, D of 512), so each activation row fetched
  *                         serves twice the weight bytes; 0: 256 weight rows. Outputs agree within
- *                         rounding (the k-chunks run in another rotated order). */
+ *                         rounding (the k-chunks run in another rotated order).
+ *   "generate_timed_from" 1 (default): the generation time rbt_hip_generate* report (ms_out[1]) covers
+ *                         generated steps g = 1 .. n_gen - 1 (step g forwards token g - 1); g0 > 1:
+ *                         steps g0 .. n_gen - 1 only (0 ms if none), e.g. the last K steps of a run. */
 int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value);
 
 /* Upload a whole .rbt2 image (e.g. the engine's mmap, rabbit2.c:129-156) to HBM once. Validates the
@@ -118,16 +122,18 @@ int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]);
 int rbt_hip_expert_stats(rbt_hip *h, uint64_t stats[6]);
 /* Device view of layer `layer` of the uploaded model (for the _dev calls). */
 int rbt_hip_layer(rbt_hip *h, int layer, rbt_moe_layer *out);
-/* The grouped (prefill) path's HBM layout (no counterpart in the reference: an optimisation of the
- * device copy). The 128-row grouped GEMMs stream a layer's experts tile by tile; in the engine's
- * row-major blobs each step of a tile spans 256 rows 4 KiB apart, which HBM serves at ~5 TB/s.
- * rbt_hip_prefill_layout keeps a second copy of layer L's experts (the same 3 * H * D bf16 per expert)
- * in tile order, each step contiguous (~7 TB/s); L NULL: every layer of the loaded model, which
- * rbt_hip_upload / rbt_hip_upload_file build by themselves while the device has room (option
- * "prefill_layout"). bf16 experts, dim a multiple of 256, expert_hidden of 256. The copy is taken
- * from the blobs now, on the handle stream: after they change, call it again. Keyed by L->experts;
- * dropped with the model, by rbt_hip_prefill_layout_drop (L NULL: all) or rbt_hip_free. Outputs are
- * bit for bit the same with or without it. */
+/* An opt-in second HBM layout for the grouped (prefill) path (no counterpart in the reference: an
+ * optimisation of the device copy, never made unless asked for here). The 128-row grouped GEMMs
+ * stream a layer's experts tile by tile; in the engine's row-major blobs each step of a tile spans
+ * 256 rows 4 KiB apart. rbt_hip_prefill_layout keeps a second copy of layer L's experts (the same
+ * 3 * H * D bf16 per expert, +12.9 GB for all 16 OLMoE-1B-7B layers) in tile order, each step
+ * contiguous; L NULL: every layer of the loaded model. bf16 experts, dim a multiple of 256,
+ * expert_hidden of 256. The copy is taken from the blobs now, on the handle stream. Writes made
+ * through this library (rbt_hip_h2d, rbt_hip_memset_dev, rbt_hip_fill_normal) into a layer's blobs
+ * retake the experts they touch, in place, after the write; after a write made any other way, call
+ * rbt_hip_prefill_layout again. Keyed by L->experts; dropped with the model, when rbt_hip_malloc
+ * returns memory that held its blobs, by rbt_hip_prefill_layout_drop (L NULL: all) or rbt_hip_free.
+ * Outputs are bit for bit the same with or without it. */
 int rbt_hip_prefill_layout(rbt_hip *h, const rbt_moe_layer *L);
 int rbt_hip_prefill_layout_drop(rbt_hip *h, const rbt_moe_layer *L);
 
@@ -190,7 +196,8 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
  * position 0, then up to n_gen tokens (at most ctx - n_prompt; the eos token is kept and ends the
  * output, -1 = none) into out; *n_out = the count. The loop runs on the device: each step's argmax
  * writes the next step's token, and each step is one HIP graph replay (steps after an eos are run and
- * discarded). ms_out (may be NULL) receives [prompt ms, generation ms] from HIP events. */
+ * discarded). ms_out (may be NULL) receives [prompt ms, generation ms] from HIP events: the prompt up to
+ * the first generated token, then the steps after it (from option "generate_timed_from" on). */
 int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
                      int *n_out, double *ms_out);
 
@@ -282,6 +289,12 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
  * events). rbt_hip_profile_get fails for an unknown name. */
 int rbt_hip_profile_enable(rbt_hip *h, int on);
 int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64_t *launches);
+/* Host only (no device needed): 1 if a ROCm profiler tool is attached to this process, as its launcher
+ * announces in the environment (rocprofv3: ROCPROFILER_LIBRARY_CTOR, ROCPROF_OUTPUT_PATH; older
+ * tools: HSA_TOOLS_LIB, ROCP_TOOL_LIB), else 0. While one is, rbt_hip_generate, rbt_hip_generate_stream
+ * and rbt_hip_generate_batch fail with a message instead of replaying HIP graphs (traced graph replays
+ * have ended in a host SIGSEGV inside the tool); the eager calls trace normally. */
+int rbt_hip_profiler_attached(void);
 
 /* Synthetic data (no counterpart in the reference, whose random weights come from NumPy,
  * rabbit2/ref/reference.py:20-50): dst[i] = offset + scale * N(0,1) sample (first + i) of stream

@@ -7,7 +7,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include <fcntl.h>
@@ -131,6 +133,7 @@ struct rbt_hip {
     int prefill_min_tokens = kPrefillMinTokensDefault;  // option "prefill_min_tokens"
     int prefill_tile_rows = 0;  // option "prefill_tile_rows": rows per grouped-GEMM tile, 0 = by batch
     bool prefill_wide = true;   // option "prefill_wide": 128-row tiles 512 weight rows wide
+    int gen_timed_from = 1;     // option "generate_timed_from": first generated step of ms_out[1]
     const int32_t *expert_counts = nullptr;  // histogram of the last grouped-path call
     // staging for the host-pointer entry points: device buffer and its pinned host twin
     void *stage = nullptr;
@@ -147,7 +150,7 @@ struct rbt_hip {
     // this device's scratch array (rbt_hip_moe_dev_noalloc), from hipGetSymbolAddress at init
     void *scratch = nullptr;
     // tiled copies of layers' experts for the 128-row grouped GEMMs (rbt_hip_prefill_layout), keyed by
-    // the layer's expert blobs; option "prefill_layout" (default 1) uses them and builds them at upload
+    // the layer's expert blobs; built only when the caller asks, used while option "prefill_layout" is on
     std::vector<TiledLayer> tiled;
     int prefill_layout = 1;
     // expert residency counters in the engine's cache-stats terms (rabbit2.c:745-751): every expert is
@@ -286,7 +289,8 @@ struct ModelLayout {
 };
 
 // Fills *m for config c when its image ends at or before `limit` bytes; returns 0 (with *end_out =
-// the image end, saturated to 2^64 - 1) otherwise, before allocating anything per layer. Layers after
+// the image end, saturated to 2^64 - 1) otherwise, before allocating anything per layer, and -1 when
+// the host cannot hold the per-layer table. Layers after
 // the first start 4 KiB aligned (the previous experts end so), so all of them have the first aligned
 // layer's size and the end has a closed form; every layer holds at least one 4 KiB expert stride, so
 // a layout that fits has at most limit / 4096 layers.
@@ -309,7 +313,12 @@ int layout_of(const rbt_config &c, uint64_t limit, ModelLayout *m, uint64_t *end
     m->final_norm = (uint64_t)final_norm;
     m->lm_head = (uint64_t)lm_head;
     m->layout_end = (uint64_t)end;
-    m->layers.assign((size_t)c.n_layers, LayerOff{});
+    try {
+        m->layers.assign((size_t)c.n_layers, LayerOff{});
+    } catch (const std::bad_alloc &) {
+        m->layers.clear();
+        return -1;
+    }
     u128 at = off;
     for (int l = 0; l < c.n_layers; l++) at = layer_offsets(c, at, stride, &m->layers[(size_t)l]);
     return 1;
@@ -468,7 +477,9 @@ int parse_header(ModelLayout *m, const unsigned char *d, uint64_t file_size, rbt
     memcpy(&c, d + 8, sizeof c);
     if (!config_ok(c)) return fail(err_h, "invalid config in header");
     uint64_t end = 0;
-    if (!layout_of(c, file_size, m, &end))
+    const int r = layout_of(c, file_size, m, &end);
+    if (r < 0) return fail(err_h, "no host memory for the layout of %d layers", c.n_layers);
+    if (!r)
         return fail(err_h, "file too small for its own config (%llu < %llu)", (unsigned long long)file_size,
                     (unsigned long long)end);
     return 1;
@@ -496,6 +507,27 @@ void tiled_drop(rbt_hip *h, const uint8_t *lo, const uint8_t *hi) {
             keep.push_back(t);
     }
     h->tiled.swap(keep);
+}
+
+// Retakes, asynchronously on the handle stream after the write that called it, every tiled copy whose
+// blobs overlap the device bytes [dst, dst + bytes) that a library call has just written (rbt_hip_h2d,
+// rbt_hip_memset_dev, rbt_hip_fill_normal): only the experts the write touched, in place, so later
+// calls and graphs captured earlier read the new weights.
+int tiled_follow_write(rbt_hip *h, const void *dst, uint64_t bytes) {
+    const uint8_t *lo = static_cast<const uint8_t *>(dst);
+    for (const TiledLayer &t : h->tiled) {
+        const uint8_t *b = static_cast<const uint8_t *>(t.experts);
+        const uint64_t span = (uint64_t)t.E * t.stride;
+        if (lo >= b + span || lo + bytes <= b) continue;
+        const uint64_t first = lo > b ? (uint64_t)(lo - b) : 0;
+        const uint64_t last = std::min<uint64_t>(span, (uint64_t)(lo + bytes - b)) - 1;
+        const int e0 = (int)(first / t.stride), e1 = (int)(last / t.stride) + 1;
+        Launch Lx;
+        Lx.s = h->stream;
+        HIP_OK(h, launch_prefill_layout(Lx, b + (uint64_t)e0 * t.stride, t.stride, e1 - e0, t.D, t.H,
+                                        static_cast<uint8_t *>(t.buf) + (uint64_t)e0 * prefill_layout_bytes(1, t.D, t.H)));
+    }
+    return 1;
 }
 
 // Builds (or rebuilds in place) the tiled copy of layer L's experts, asynchronously on the handle stream.
@@ -567,6 +599,8 @@ int model_alloc(rbt_hip *h, const ModelLayout &m) {
     HIP_OK(h, hipMalloc(&p, m.layout_end));
     h->model = static_cast<uint8_t *>(p);
     h->model_size = m.layout_end;
+    // a copy keyed inside fresh memory belongs to blobs freed earlier (the stream is idle: model_drop)
+    tiled_drop(h, h->model, h->model + h->model_size);
     return 1;
 }
 
@@ -776,8 +810,26 @@ int enqueue_step(rbt_hip *h, bool final) {
     return 1;
 }
 
-// Captures `n` enqueued steps of one kind into an executable graph.
+// The environment variable through which a ROCm profiler tool announces itself to this process, or
+// nullptr. rocprofv3's launcher exports ROCPROFILER_LIBRARY_CTOR and ROCPROF_OUTPUT_PATH to the program
+// it starts; the older rocprof tools load through HSA_TOOLS_LIB / ROCP_TOOL_LIB.
+const char *profiler_var() {
+    static const char *const vars[] = {"ROCPROFILER_LIBRARY_CTOR", "ROCPROF_OUTPUT_PATH", "HSA_TOOLS_LIB",
+                                       "ROCP_TOOL_LIB"};
+    for (const char *v : vars) {
+        const char *val = getenv(v);
+        if (val && *val) return v;
+    }
+    return nullptr;
+}
+
+// Captures `n` enqueued steps of one kind into an executable graph. Graph replay is refused while a
+// profiler tool is attached: replays traced by rocprofv3 have ended in a host SIGSEGV inside the
+// tool's interception of hipGraphLaunch, so a profiled run must take the eager paths.
 int capture_step(rbt_hip *h, bool final, hipGraphExec_t *exec) {
+    if (const char *v = profiler_var())
+        return fail(h, "HIP graph replay is off while a profiler tool is attached (%s is set): profile the "
+                       "eager calls (rbt_hip_forward, rbt_hip_forward_batch, rbt_hip_moe_dev) instead", v);
     hipGraph_t g = nullptr;
     HIP_OK(h, hipStreamBeginCapture(h->stream, hipStreamCaptureModeRelaxed));
     const int ok = enqueue_step(h, final);
@@ -982,29 +1034,12 @@ int rbt_hip_set_router_order(rbt_hip *h, int order) {
     return 1;
 }
 
-// The tiled copies of every layer of the uploaded model. at_upload: only with option "prefill_layout"
-// on, for a shape that has one and while the device keeps 1 GiB free besides; nothing built is no
-// error there (the grouped GEMMs then read the blobs).
-int tiled_build_model(rbt_hip *h, bool at_upload) {
+// The tiled copies of every layer of the loaded model (rbt_hip_prefill_layout with L NULL).
+int tiled_build_model(rbt_hip *h) {
     const rbt_config &c = h->cfg;
-    if (at_upload) {
-        if (!h->prefill_layout || c.dtype != RBT_DT_BF16 || !prefill_layout_supported(c.dtype, c.dim, c.expert_hidden))
-            return 1;
-        size_t free_b = 0, total_b = 0;
-        if (hipMemGetInfo(&free_b, &total_b) != hipSuccess ||
-            free_b < (size_t)c.n_layers * prefill_layout_bytes(c.n_experts, c.dim, c.expert_hidden) + (1ull << 30))
-            return 1;
-    }
     for (int l = 0; l < c.n_layers; l++) {
         rbt_moe_layer ml;
-        if (!rbt_hip_layer(h, l, &ml) || !tiled_build(h, &ml)) {
-            if (!at_upload) return 0;
-            // at upload the copies are an optimisation: without them the model is complete
-            (void)hipStreamSynchronize(h->stream);
-            tiled_drop(h, h->model, h->model + h->model_size);
-            h->err[0] = '\0';
-            return 1;
-        }
+        if (!rbt_hip_layer(h, l, &ml) || !tiled_build(h, &ml)) return 0;
     }
     return 1;
 }
@@ -1024,7 +1059,7 @@ int rbt_hip_upload(rbt_hip *h, const void *file, uint64_t file_size, rbt_config 
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
-    return tiled_build_model(h, true);
+    return 1;
 }
 
 int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
@@ -1066,7 +1101,7 @@ int rbt_hip_upload_file(rbt_hip *h, const char *path, rbt_config *cfg) {
     h->cache_hits = 0;
     h->cache_misses = (uint64_t)c.n_layers * c.n_experts;
     if (cfg) *cfg = c;
-    return tiled_build_model(h, true);
+    return 1;
 }
 
 int rbt_hip_file_info(const char *path, rbt_config *cfg, uint64_t info[7]) {
@@ -1116,7 +1151,7 @@ int rbt_hip_prefill_layout(rbt_hip *h, const rbt_moe_layer *L) {
     if (!set_device(h)) return 0;
     if (L) return tiled_build(h, L);
     if (!h->model) return fail(h, "prefill_layout: no model (pass a layer, or upload a model first)");
-    return tiled_build_model(h, false);
+    return tiled_build_model(h);
 }
 
 int rbt_hip_prefill_layout_drop(rbt_hip *h, const rbt_moe_layer *L) {
@@ -1138,10 +1173,15 @@ int rbt_hip_model_create(rbt_hip *h, const rbt_config *cfg, void **model_dev) {
     *model_dev = nullptr;
     if (!config_ok(*cfg)) return fail(h, "model_create: invalid config");
     ModelLayout m;
-    uint64_t end = 0;
-    if (!layout_of(*cfg, kMaxImageBytes, &m, &end))
-        return fail(h, "model_create: the image of this config (%llu bytes) exceeds %llu bytes",
-                    (unsigned long long)end, (unsigned long long)kMaxImageBytes);
+    uint64_t end = 0, limit = kMaxImageBytes;
+    if (!set_device(h)) return 0;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) == hipSuccess && total_b < limit) limit = total_b;
+    const int r = layout_of(*cfg, limit, &m, &end);
+    if (r < 0) return fail(h, "model_create: no host memory for the layout of %d layers", cfg->n_layers);
+    if (!r)
+        return fail(h, "model_create: the image of this config (%llu bytes) exceeds the device's %llu bytes",
+                    (unsigned long long)end, (unsigned long long)limit);
     if (!model_alloc(h, m)) return 0;
     adopt_layout(h, std::move(m));
     h->cache_hits = 0;
@@ -1312,6 +1352,14 @@ int rbt_hip_malloc(rbt_hip *h, void **dev, uint64_t bytes) {
     *dev = nullptr;
     if (!set_device(h)) return 0;
     HIP_OK(h, hipMalloc(dev, bytes ? bytes : 1));
+    const uint8_t *p = static_cast<const uint8_t *>(*dev);
+    for (const TiledLayer &t : h->tiled)
+        if (static_cast<const uint8_t *>(t.experts) >= p && static_cast<const uint8_t *>(t.experts) < p + bytes) {
+            // copies of blobs freed earlier (their memory is this allocation now): drop them
+            HIP_OK(h, hipStreamSynchronize(h->stream));
+            tiled_drop(h, p, p + bytes);
+            break;
+        }
     return 1;
 }
 
@@ -1320,6 +1368,11 @@ int rbt_hip_free_dev(rbt_hip *h, void *dev) {
     if (!dev) return 1;
     if (!set_device(h)) return 0;
     HIP_OK(h, hipStreamSynchronize(h->stream));
+    // tiled copies of blobs inside the freed allocation go with it
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (!h->tiled.empty() && hipMemGetAddressRange(&base, &size, static_cast<hipDeviceptr_t>(dev)) == hipSuccess)
+        tiled_drop(h, static_cast<const uint8_t *>(base), static_cast<const uint8_t *>(base) + size);
     HIP_OK(h, hipFree(dev));
     return 1;
 }
@@ -1330,6 +1383,7 @@ int rbt_hip_h2d(rbt_hip *h, void *dst_dev, const void *src, uint64_t bytes) {
     if (!dst_dev || !src) return fail(h, "h2d: NULL pointer");
     if (!set_device(h)) return 0;
     HIP_OK(h, hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, h->stream));
+    if (!tiled_follow_write(h, dst_dev, bytes)) return 0;
     HIP_OK(h, hipStreamSynchronize(h->stream));
     return 1;
 }
@@ -1350,7 +1404,7 @@ int rbt_hip_memset_dev(rbt_hip *h, void *dst_dev, int value, uint64_t bytes) {
     if (!dst_dev) return fail(h, "memset: NULL pointer");
     if (!set_device(h)) return 0;
     HIP_OK(h, hipMemsetAsync(dst_dev, value, bytes, h->stream));
-    return 1;
+    return tiled_follow_write(h, dst_dev, bytes);
 }
 
 int rbt_hip_synchronize(rbt_hip *h) {
@@ -1389,6 +1443,9 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
         h->prefill_tile_rows = (int)value;
     } else if (strcmp(name, "prefill_wide") == 0) {
         h->prefill_wide = value != 0;
+    } else if (strcmp(name, "generate_timed_from") == 0) {
+        if (value < 1 || value > (1 << 30)) return fail(h, "set_option: generate_timed_from must be in [1, 2^30]");
+        h->gen_timed_from = (int)value;
     } else {
         return fail(h, "set_option: unknown option '%s'", name);
     }
@@ -1396,6 +1453,8 @@ int rbt_hip_set_option(rbt_hip *h, const char *name, int64_t value) {
 }
 
 void *rbt_hip_stream(rbt_hip *h) { return h ? static_cast<void *>(h->stream) : nullptr; }
+
+int rbt_hip_profiler_attached(void) { return profiler_var() != nullptr; }
 
 int rbt_hip_profile_enable(rbt_hip *h, int on) {
     if (!h) return fail(nullptr, "profile: handle is NULL");
@@ -1449,7 +1508,7 @@ int rbt_hip_fill_normal(rbt_hip *h, void *dst_dev, int dtype, uint64_t n, uint64
     if (!dst_dev) return fail(h, "fill_normal: NULL pointer");
     if (!set_device(h)) return 0;
     HIP_OK(h, launch_fill_normal(lc(h, -1), dst_dev, dtype, n, seed, stream, first, scale, offset));
-    return 1;
+    return tiled_follow_write(h, dst_dev, n * (dtype == RBT_DT_BF16 ? 2 : 4));
 }
 
 int rbt_hip_state_init(rbt_hip *h, int ctx) { return rbt_hip_batch_init(h, 1, ctx); }
@@ -1616,7 +1675,9 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
     const int prof = h->prof.mode;
     h->prof.mode = 0;
     hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
-    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    // ev: start, after the first generated token, end, start of the timed window (ms_out[1])
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    const int t0 = h->gen_timed_from;
     // streaming: one event per step in flight; the host keeps at most kStreamAhead steps queued past
     // the last token it has reported, and stops queueing at the eos token
     constexpr int kStreamAhead = 32;
@@ -1636,16 +1697,26 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
         return 0;
     }
     hipError_t e = hipSuccess;
-    for (int i = 0; i < 3 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
+    for (int i = 0; i < 4 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
     if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[0], h->stream));
     // the prompt: n_prompt forwards, the last one with lm_head + argmax (the first generated token)
     for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = HIP_TRY(hipGraphLaunch(g_adv, h->stream));
     int n = n_gen;
+    bool window = false;  // ev[3] recorded: before generated step t0, else with ev[2]
+    auto mark_window = [&](int g) -> hipError_t {
+        if (window || g < t0) return hipSuccess;
+        window = true;
+        return HIP_TRY(hipEventRecord(ev[3], h->stream));
+    };
     if (!on_token) {
         if (e == hipSuccess && n_gen > 0) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
         if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[1], h->stream));
         // each further token: one forward of the previous one (rabbit2.c:733)
-        for (int g = 1; g < n_gen && e == hipSuccess; g++) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        for (int g = 1; g < n_gen && e == hipSuccess; g++) {
+            e = mark_window(g);
+            if (e == hipSuccess) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        }
+        if (e == hipSuccess) e = mark_window(INT32_MAX);
         if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
         if (e == hipSuccess && n_gen > 0)
             e = HIP_TRY(hipMemcpyAsync(out, h->ds.seq + n_prompt, 4 * (size_t)n_gen, hipMemcpyDeviceToHost, h->stream));
@@ -1660,7 +1731,8 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
         int queued = 0, reported = 0;
         bool more = n_gen > 0, report = true;
         auto queue_step = [&](int g) -> hipError_t {
-            hipError_t r = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+            hipError_t r = g > 0 ? mark_window(g) : hipSuccess;
+            if (r == hipSuccess) r = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
             if (r == hipSuccess && g == 0) r = HIP_TRY(hipEventRecord(ev[1], h->stream));
             if (r == hipSuccess)
                 r = HIP_TRY(hipMemcpyAsync(h->tok_host + g, h->ds.seq + n_prompt + g, 4, hipMemcpyDeviceToHost,
@@ -1673,6 +1745,7 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
             while (e == hipSuccess && more && queued < reported + kStreamAhead) {
                 e = queue_step(queued++);
                 if (queued == n_gen) more = false;
+                if (!more && e == hipSuccess) e = mark_window(INT32_MAX);
                 if (!more && e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
             }
             if (e != hipSuccess || reported == queued) break;
@@ -1685,20 +1758,22 @@ int rbt_hip_generate_stream(rbt_hip *h, const int32_t *prompt, int n_prompt, int
             if (tok == eos || !report) {  // nothing more is queued; the queued steps run to their end
                 if (more) {
                     more = false;
-                    e = HIP_TRY(hipEventRecord(ev[2], h->stream));
+                    e = mark_window(INT32_MAX);
+                    if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
                 }
                 break;
             }
         }
         if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
         if (n_gen == 0 && e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[1], h->stream));
+        if (n_gen == 0 && e == hipSuccess) e = mark_window(INT32_MAX);
         if (n_gen == 0 && e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
         if (e == hipSuccess) e = HIP_TRY(hipStreamSynchronize(h->stream));
     }
     if (e == hipSuccess && ms_out) {
         float a = 0.0f, b = 0.0f;
         e = HIP_TRY(hipEventElapsedTime(&a, ev[0], ev[1]));
-        if (e == hipSuccess) e = HIP_TRY(hipEventElapsedTime(&b, ev[1], ev[2]));
+        if (e == hipSuccess) e = HIP_TRY(hipEventElapsedTime(&b, ev[3], ev[2]));
         ms_out[0] = a;
         ms_out[1] = b;
     }
@@ -1762,17 +1837,27 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
     const int prof = h->prof.mode;
     h->prof.mode = 0;
     hipGraphExec_t g_adv = nullptr, g_fin = nullptr;
-    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    // ev: start, after the first generated step, end, start of the timed window (ms_out[1])
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    const int t0 = h->gen_timed_from;
     int ok = capture_step(h, false, &g_adv) && capture_step(h, true, &g_fin);
     h->prof.mode = prof;
     hipError_t e = hipSuccess;
     if (ok) {
-        for (int i = 0; i < 3 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
+        for (int i = 0; i < 4 && e == hipSuccess; i++) e = HIP_TRY(hipEventCreate(&ev[i]));
         if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[0], h->stream));
         for (int p = 0; p + 1 < n_prompt && e == hipSuccess; p++) e = HIP_TRY(hipGraphLaunch(g_adv, h->stream));
         if (e == hipSuccess && n_gen > 0) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
         if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[1], h->stream));
-        for (int g = 1; g < n_gen && e == hipSuccess; g++) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        bool window = false;
+        for (int g = 1; g < n_gen && e == hipSuccess; g++) {
+            if (!window && g >= t0) {
+                window = true;
+                e = HIP_TRY(hipEventRecord(ev[3], h->stream));
+            }
+            if (e == hipSuccess) e = HIP_TRY(hipGraphLaunch(g_fin, h->stream));
+        }
+        if (e == hipSuccess && !window) e = HIP_TRY(hipEventRecord(ev[3], h->stream));
         if (e == hipSuccess) e = HIP_TRY(hipEventRecord(ev[2], h->stream));
         for (int b = 0; b < B && e == hipSuccess && n_gen > 0; b++)
             e = HIP_TRY(hipMemcpyAsync(out + (size_t)b * n_gen, h->ds.seq + (size_t)b * ctx + n_prompt,
@@ -1781,7 +1866,7 @@ int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int
         if (e == hipSuccess && ms_out) {
             float a = 0.0f, bms = 0.0f;
             e = HIP_TRY(hipEventElapsedTime(&a, ev[0], ev[1]));
-            if (e == hipSuccess) e = HIP_TRY(hipEventElapsedTime(&bms, ev[1], ev[2]));
+            if (e == hipSuccess) e = HIP_TRY(hipEventElapsedTime(&bms, ev[3], ev[2]));
             ms_out[0] = a;
             ms_out[1] = bms;
         }

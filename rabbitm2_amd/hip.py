@@ -24,7 +24,7 @@ EXPORTS = (
     "rbt_hip_model_create", "rbt_hip_tensor", "rbt_hip_upload_file", "rbt_hip_expert_stats", "rbt_hip_batch_init",
     "rbt_hip_forward_batch", "rbt_hip_generate_batch", "rbt_hip_set_sampling", "rbt_hip_file_info",
     "rbt_hip_generate_stream", "rbt_hip_routing_history", "rbt_hip_expert_cache_replay",
-    "rbt_hip_moe_dev_noalloc", "rbt_hip_prefill_layout", "rbt_hip_prefill_layout_drop",
+    "rbt_hip_moe_dev_noalloc", "rbt_hip_prefill_layout", "rbt_hip_prefill_layout_drop", "rbt_hip_profiler_attached",
 )
 
 TOKEN_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32)
@@ -100,6 +100,7 @@ def lib():
         L.rbt_hip_routing_history.argtypes = [vp, i32, i32, i32, vp]
         L.rbt_hip_expert_cache_replay.argtypes = [u64, u64, i32, i32, i32, vp, u64, C.POINTER(C.c_uint64)]
         L.rbt_hip_file_info.argtypes = [C.c_char_p, C.POINTER(Config), C.POINTER(C.c_uint64)]
+        L.rbt_hip_profiler_attached.argtypes = []
         _lib = L
     return _lib
 
@@ -364,6 +365,12 @@ class Device:
     def matvec_dev(self, out, W, dtype, x, rows, cols):
         self._check(self.L.rbt_hip_matvec_dev(self.h, out.p, W if isinstance(W, C.c_void_p) else W.p, dtype, x.p,
                                               rows, cols))
+
+
+def profiler_attached():
+    """True while a ROCm profiler tool is attached to this process (rbt_hip_profiler_attached): the
+    library then refuses HIP graph replay, and so should a host that captures graphs of its own."""
+    return bool(lib().rbt_hip_profiler_attached())
 
 
 def expert_cache_replay(budget_bytes, expert_stride, routing, n_experts):

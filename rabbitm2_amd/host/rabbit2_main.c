@@ -57,6 +57,29 @@ static void usage(const char *p) {
             p, p, p);
 }
 
+/* "moe: bytes=... GB/s=... %peak=...": the MoE blocks the library timed on the device with its deferred
+ * HIP events (profiling mode 2; the --dump pass's eager forward() steps, at most 4096 blocks: the
+ * --gen loop replays HIP graphs, whose kernels HIP does not time), their bytes as the engine's block
+ * reads them (router rows and top_k experts' w1/w3/w2 per token and layer), against MI355X's published
+ * 8 TB/s HBM peak. Nothing is printed when no block was timed. */
+static int print_moe_line(rbt_hip *h, const rbt_config *c) {
+    static const char *const kern[4] = {"router", "topk", "gateup", "down_combine"};
+    double ms = 0.0, t = 0.0;
+    uint64_t blocks = 0, n = 0;
+    for (int i = 0; i < 4; i++) {
+        if (!rbt_hip_profile_get(h, kern[i], &t, &n)) return 0;
+        ms += t;
+        if (i == 0) blocks = n;
+    }
+    if (!blocks) return 1;
+    const double esz = c->dtype == RBT_DT_BF16 ? 2.0 : 4.0;
+    const double bytes =
+        (double)blocks * esz * ((double)c->n_experts * c->dim + 3.0 * c->top_k * c->expert_hidden * (double)c->dim);
+    const double gbs = ms > 0.0 ? bytes / (ms * 1e-3) / 1e9 : 0.0;
+    fprintf(stderr, "moe: bytes=%.0f GB/s=%.1f %%peak=%.1f\n", bytes, gbs, 100.0 * gbs / 8000.0);
+    return 1;
+}
+
 /* The engine's gen-loop output: one id per line, flushed (rabbit2.c:728-729). */
 static int print_token(void *user, int32_t token) {
     (void)user;
@@ -80,6 +103,7 @@ static int run(const char *path, const rbt_config *c, uint64_t expert_stride, in
     if (!rbt_hip_set_router_order(h, order) || !rbt_hip_upload_file(h, path, NULL)) goto done;
     if (cache_budget && !rbt_hip_set_option(h, "routing_history", 1)) goto done;
     if (!rbt_hip_state_init(h, ctx)) goto done;
+    if (!rbt_hip_profile_enable(h, 2)) goto done; /* device times of the MoE blocks, for the moe line */
 
     logits = (float *)malloc(sizeof(float) * (size_t)c->vocab);
     routing = (int32_t *)calloc((size_t)c->n_layers * c->top_k, sizeof(int32_t));
@@ -131,6 +155,7 @@ static int run(const char *path, const rbt_config *c, uint64_t expert_stride, in
     fprintf(stderr, "prompt: %d tokens in %.2fs (%.2f tok/s)", nt, t1 - t0, nt / (t1 - t0 + 1e-9));
     if (gen > 0) fprintf(stderr, " | generated %d in %.2fs (%.2f tok/s)", produced, t2 - t1, produced / (t2 - t1 + 1e-9));
     fprintf(stderr, "\n");
+    if (!print_moe_line(h, c)) goto done;
     if (cache_budget) {
         /* the forward() calls the engine makes: the prompt, then one per generated id but the last
          * (rabbit2.c:704, :732-733) */

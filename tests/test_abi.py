@@ -4,6 +4,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -54,3 +55,35 @@ def test_init_without_a_device_reports_an_error():
     h = ctypes.c_void_p()
     assert hip.lib().rbt_hip_init(ctypes.byref(h), 0) == 0
     assert b"no HIP device" in hip.lib().rbt_hip_last_error(None) or b"init" in hip.lib().rbt_hip_last_error(None)
+
+
+PROFILER_VARS = ("ROCPROFILER_LIBRARY_CTOR", "ROCPROF_OUTPUT_PATH", "HSA_TOOLS_LIB", "ROCP_TOOL_LIB")
+
+
+def _attached_in_child(extra_env):
+    """rbt_hip_profiler_attached() in a fresh process whose environment is ours without any profiler
+    variable, plus extra_env (the library reads the variables when asked, no device is touched)."""
+    env = {k: v for k, v in os.environ.items() if k not in PROFILER_VARS}
+    env.update(extra_env)
+    code = ("import ctypes, sys; L = ctypes.CDLL(sys.argv[1]); print(L.rbt_hip_profiler_attached())")
+    out = subprocess.run([sys.executable, "-c", code, hip.LIB_PATH], env=env, capture_output=True, text=True,
+                         check=True)
+    return int(out.stdout.strip())
+
+
+@pytest.mark.parametrize("var", PROFILER_VARS)
+def test_profiler_detection(var):
+    assert _attached_in_child({}) == 0
+    assert _attached_in_child({var: "1"}) == 1
+    assert _attached_in_child({var: ""}) == 0  # set but empty: no tool
+
+
+def test_bench_refuses_graph_replay_under_a_profiler():
+    """bench.py's graph-replayed legs exit non-zero with a message when a profiler tool is attached,
+    before anything touches a device."""
+    env = {k: v for k, v in os.environ.items() if k not in PROFILER_VARS}
+    env["ROCPROF_OUTPUT_PATH"] = "/tmp/unused"
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--no-cpu"], env=env, capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 2
+    assert "profiler" in res.stderr and "--profile-" in res.stderr

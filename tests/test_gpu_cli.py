@@ -211,3 +211,45 @@ def test_reference_engine_with_the_hip_seam(tmp_path, case):
     assert res.returncode == 0, res.stderr
     assert [int(t) for t in res.stdout.split()] == fx[f"gen_{tag}"].tolist()
     print(f"{case}: routing identical, worst logits error {worst:.2e}", flush=True)
+
+
+def write_sparse_header(path, **kw):
+    """A .rbt2 header of these config fields (the reference's Config defaults for the rest,
+    rabbit2/ref/rbt2.py:28-44) in a sparse file exactly as long as its layout: zero weights."""
+    import struct
+    d = dict(vocab=256, dim=64, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=16, n_experts=8, top_k=2,
+             expert_hidden=128, max_seq=64, dtype=po.DT_F32, qk_norm=0, norm_topk=1)
+    d.update(kw)
+    cfg = po.Config(**d)
+    with open(path, "wb") as f:
+        f.write(b"RBT2" + struct.pack("<I", 2) + bytes(cfg))
+        f.truncate(po.layout(cfg)["end"])
+    return cfg
+
+
+@pytest.mark.parametrize("binary", ["cli", "patched"])
+def test_expert_read_beyond_4gib(tmp_path, binary):
+    """The reference's sparse-file case (rabbit2/tests/test_engine_cache.py:80-97): 1,048,576 zero
+    experts per layer, so layer 1's experts start past 4 GiB (an 8 GiB image uploaded to HBM), top-1,
+    --expert-cache-mib 1: the stats line reports misses=2 and the routing file holds (0, 0) -- every
+    logit is 0, and the lowest index wins the tie. Also its 'budget too small' exit (:72-78)."""
+    exe = CLI if binary == "cli" else PATCHED
+    if not os.path.exists(exe):
+        pytest.skip("patched reference engine not built (oracle/Makefile ref_hip)")
+    path = tmp_path / "sparse.rbt2"
+    cfg = write_sparse_header(path, vocab=8, dim=2, n_layers=2, n_heads=1, n_kv_heads=1, head_dim=2,
+                              n_experts=1048576, top_k=1, expert_hidden=1, max_seq=2)
+    assert po.layout(cfg)["layers"][1]["experts"] > 2**32
+    kernel = ["--kernel", "hip"] if binary == "patched" else []
+    print(f"{binary}: 8 GiB sparse image, --dump --expert-cache-mib 1", flush=True)
+    res = subprocess.run([exe, str(path), "--dump", str(tmp_path / "logits"), str(tmp_path / "routing"),
+                          "--expert-cache-mib", "1"] + kernel + ["1"], capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr
+    assert "misses=2" in res.stderr
+    assert np.fromfile(tmp_path / "routing", dtype="<i4").tolist() == [0, 0]
+    small = tmp_path / "small.rbt2"
+    write_sparse_header(small, vocab=8, dim=1024, n_layers=1, n_heads=1, n_kv_heads=1, head_dim=2, n_experts=1,
+                        top_k=1, expert_hidden=512, max_seq=2)  # one expert is 6 MiB: more than the 1 MiB budget
+    res = subprocess.run([exe, str(small), "--gen", "1", "--expert-cache-mib", "1"] + kernel + ["1"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode != 0 and "budget too small" in res.stderr, res.stderr

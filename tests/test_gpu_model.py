@@ -115,3 +115,17 @@ def test_rejected_upload_keeps_the_loaded_model(dev, tmp_path):
         dev.upload_file(str(short))
     for pos in range(half, len(tokens)):
         step(pos)
+
+
+def test_model_create_rejects_images_beyond_the_device(dev):
+    """rbt_hip_model_create bounds the image by the device's memory before it builds the per-layer
+    table: 2^31 - 1 layers of a tiny config (about 10 TB of image) fail with a message, and the handle
+    stays usable."""
+    from rabbitm2_amd import hip as rh
+    big = rh.Config(vocab=1, dim=2, n_layers=2**31 - 1, n_heads=1, n_kv_heads=1, head_dim=2, n_experts=1, top_k=1,
+                    expert_hidden=1, max_seq=1, dtype=po.DT_F32, qk_norm=0, norm_topk=0, rope_theta=1e4,
+                    rms_eps=1e-5)
+    with pytest.raises(rh.HipError, match="exceeds the device"):
+        dev.model_create(big)
+    cfg, gp = MODELS["odd_f32"]
+    assert dev.upload(po.build_model(cfg, gp)).dim == cfg.dim

@@ -210,18 +210,24 @@ def test_prefill_tile_rows_option_checked(dev):
             dev.set_option("prefill_tile_rows", bad)
 
 
-@pytest.mark.parametrize("rows", [64, 128])
+@pytest.mark.parametrize("rows,wide,shape", [(64, 1, "olmoe"), (128, 1, "olmoe"), (128, 0, "olmoe"),
+                                             (0, 1, "d768-h512")],
+                         ids=["64-row", "128-row-wide", "128-row-256wide", "d768-h512-default"])
 @pytest.mark.parametrize("biased", [False, True], ids=["uniform", "skewed"])
-def test_tiled_expert_copy_is_bitwise_the_blobs(dev, grouped_from, tile_rows, biased, rows):
-    """The OLMoE layer at 512 tokens on 64- and 128-row tiles, reading the experts from the row-major
-    blobs and from the tiled copy (rbt_hip_prefill_layout): identical outputs, both held to the oracle;
-    a dropped copy is no longer read."""
+def test_tiled_expert_copy_is_bitwise_the_blobs(dev, grouped_from, tile_rows, biased, rows, wide, shape):
+    """512 tokens on 64- and 128-row tiles, reading the experts from the row-major blobs and from the
+    tiled copy (rbt_hip_prefill_layout): identical outputs, both held to the oracle; a dropped copy is
+    no longer read. The OLMoE layer runs the 64-row LDS-ring tiles, the 512-row-wide register tiles
+    and (option prefill_wide 0) the 256-row-wide ones (gemm_wr_tile); a layer with dim 768 and
+    expert_hidden 512 has no wide tiles, so its default plan runs gemm_wr_tile over the copy."""
     grouped_from(1)
     tile_rows(rows)
+    dev.set_option("prefill_wide", wide)
+    D, H = (2048, 1024) if shape == "olmoe" else (768, 512)
     bias = np.zeros(64, np.float32)
     if biased:
         bias[:8] = 2.0
-    layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=1, bias=bias)
+    layer = SynthLayer(dev, D, 64, 8, H, po.DT_BF16, 1, seed=1, bias=bias)
     try:
         xb = layer.make_x(512, seed=5)
         L = layer.desc()
@@ -235,6 +241,7 @@ def test_tiled_expert_copy_is_bitwise_the_blobs(dev, grouped_from, tile_rows, bi
         again = layer.run_gpu(xb)
         assert again["moe"].tobytes() == plain["moe"].tobytes()
     finally:
+        dev.set_option("prefill_wide", 1)
         dev.prefill_layout_drop()
         layer.close()
 
@@ -269,9 +276,10 @@ def test_wide_tiles_agree_with_256_row_tiles(dev, grouped_from, biased, T):
 
 
 def test_tiled_copy_follows_changed_blobs(dev, grouped_from, tile_rows):
-    """A copy taken before the blobs change is stale until it is taken again (the documented contract):
-    after the weights of two experts are rewritten and the copy re-taken, the output matches the
-    oracle on the new weights."""
+    """Writes made through the library into a layer's blobs carry into its tiled copy by themselves:
+    two experts rewritten by rbt_hip_fill_normal, then one expert's w1 overwritten by rbt_hip_h2d with
+    another expert's bytes; after each, the grouped output matches the oracle on the new weights, and
+    re-taking the copy changes nothing."""
     grouped_from(1)
     tile_rows(128)
     layer = SynthLayer(dev, 2048, 64, 8, 1024, po.DT_BF16, 1, seed=3)
@@ -280,11 +288,63 @@ def test_tiled_copy_follows_changed_blobs(dev, grouped_from, tile_rows):
         L = layer.desc()
         dev.prefill_layout(L)
         layer.reseed_experts([5, 40], seed=99)
+        followed, _ = check_grouped(dev, layer, xb, label="copy after fill_normal")
+        mat = layer.H * layer.D * layer.esz
+        src = layer.experts[11 * layer.stride: 11 * layer.stride + mat].copy()
+        dev.h2d(layer.experts_dev, src, offset=3 * layer.stride)
+        layer.experts = dev.d2h(layer.experts_dev, (layer.E * layer.stride,), np.uint8)
+        followed, _ = check_grouped(dev, layer, xb, label="copy after h2d")
         dev.prefill_layout(L)
-        check_grouped(dev, layer, xb, label="re-taken copy")
+        retaken = layer.run_gpu(xb)
+        assert retaken["moe"].tobytes() == followed["moe"].tobytes()
     finally:
         dev.prefill_layout_drop()
         layer.close()
+
+
+def test_model_image_writes_reach_prefill_and_decode(dev, grouped_from, tile_rows):
+    """A created model image with tiled copies of every layer (rbt_hip_prefill_layout(NULL)): an expert
+    overwritten through rbt_hip_tensor + rbt_hip_h2d changes the host-pointer MoE block (rbt_hip_moe) at
+    T = 1 (decode kernels, which read the blobs) and at T = 256 (grouped GEMMs over the copy) alike:
+    both match the oracle on the image as it is after the write."""
+    from rabbitm2_amd import hip as rh
+    grouped_from(12)
+    tile_rows(0)
+    cfg = rh.Config(vocab=64, dim=512, n_layers=2, n_heads=4, n_kv_heads=4, head_dim=128, n_experts=8, top_k=2,
+                    expert_hidden=256, max_seq=64, dtype=po.DT_BF16, qk_norm=1, norm_topk=0, rope_theta=1e4,
+                    rms_eps=1e-5)
+    base = dev.model_create(cfg)
+    img = rh.DevBuf(dev, base.value, dev.tensor("lm_head")[0] + dev.tensor("lm_head")[1])
+    dev.fill_normal(img, po.DT_BF16, img.nbytes // 2, 21, 1, scale=0.02)
+    dev.prefill_layout()
+    stride = (3 * cfg.expert_hidden * cfg.dim * 2 + 4095) // 4096 * 4096
+    r_off, r_bytes = dev.tensor("router", 1)
+    e_off, e_bytes = dev.tensor("experts", 1)
+    rng = np.random.default_rng(2)
+    xb = rng.standard_normal((256, cfg.dim)).astype(np.float32)
+
+    def check(label):
+        router = dev.d2h(img, (cfg.n_experts, cfg.dim), np.uint16, offset=r_off)
+        experts = dev.d2h(img, (e_bytes,), np.uint8, offset=e_off)
+        want = po.moe_layer(cfg.dim, cfg.n_experts, cfg.top_k, cfg.expert_hidden, po.DT_BF16, 0, router, experts,
+                            stride, xb, order=po.ORDER_AVX2)
+        for T in (1, 256):
+            x, routing = dev.moe(1, xb[:T], x=np.zeros((T, cfg.dim), np.float32))
+            assert np.array_equal(routing, want["routing"][:T]), (label, T)
+            err = normwise_err(x, want["moe"][:T])
+            print(f"{label} T={T}: moe err {err:.2e}", flush=True)
+            assert err <= MOE_RTOL
+        return want
+
+    dev.set_router_order(po.ORDER_AVX2)
+    before = check("before the write")
+    used = np.bincount(before["routing"].ravel(), minlength=cfg.n_experts)
+    e = int(np.argmax(used))  # the most used expert gets another expert's weights
+    donor = (e + 1) % cfg.n_experts
+    blob = dev.d2h(img, (stride,), np.uint8, offset=e_off + donor * stride)
+    dev.h2d(img, blob, offset=e_off + e * stride)
+    after = check("after the write")
+    assert not np.array_equal(after["moe"], before["moe"])
 
 
 def test_prefill_layout_rejects_shapes_without_one(dev):

@@ -241,3 +241,53 @@ def test_moe_layer_bias_steers_routing():
     bias[[6, 2]] = [50.0, 40.0]
     got = po.moe_layer(D, E, K, H, 1, 1, router, experts, stride, xb, bias=bias)
     assert np.all(got["routing"] == [6, 2])
+
+
+def _f64_routing(router_f64, xb, K, bias, after_softmax=False):
+    """Routing and un-renormalised weights in float64: softmax over the router logits, with `bias`
+    added to the logits before the softmax (after_softmax False) or to the probabilities after it."""
+    routes, weights = [], []
+    for x in xb.astype(np.float64):
+        logits = router_f64 @ x
+        if not after_softmax:
+            logits = logits + bias
+        p = np.exp(logits - logits.max())
+        p /= p.sum()
+        key = p + bias if after_softmax else p
+        top = np.argsort(-key, kind="stable")[:K]
+        routes.append(top)
+        weights.append(p[top])
+    return np.array(routes), np.array(weights)
+
+
+def test_moe_layer_skew_bias_goes_before_the_softmax():
+    """The skewed prefill workload's router bias (+2.0 on the logits of experts 0-7, 64 experts, top-8,
+    un-renormalised weights) against the float64 brute force. The router is scaled so that logits
+    spread over several units: some tokens then route past experts 0-7 despite the bias, which a bias
+    added to the probabilities after the softmax (always < 1 < 2.0) could never do."""
+    D, E, K, H = 64, 64, 8, 16
+    rng = np.random.default_rng(11)
+    router_f32 = (rng.standard_normal((E, D)) * (3.0 / math.sqrt(D))).astype(np.float32)
+    router = po.f32_to_bf16(router_f32).view(np.uint8).reshape(-1)
+    _, experts, stride = _random_layer(D, E, H, po.DT_BF16, seed=12)
+    xb = rng.standard_normal((64, D)).astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    bias[:8] = 2.0
+    R = po.bf16_to_f32(router.view(np.uint16)).reshape(E, D).astype(np.float64)
+    want_routes, want_w = _f64_routing(R, xb, K, bias.astype(np.float64))
+    mutant_routes, _ = _f64_routing(R, xb, K, bias.astype(np.float64), after_softmax=True)
+    unbiased_routes, _ = _f64_routing(R, xb, K, np.zeros(E))
+    hot = set(range(8))
+    # the workload is skewed (the bias moves routing) yet not degenerate (some tokens leave 0-7)
+    assert any(set(r) != hot for r in want_routes)
+    assert not np.array_equal(want_routes, unbiased_routes)
+    # the mutant routes every token to exactly 0-7, so it disagrees with the brute force
+    assert all(set(r) == hot for r in mutant_routes)
+    assert not np.array_equal(np.sort(mutant_routes, axis=1), np.sort(want_routes, axis=1))
+    for order in (po.ORDER_SCALAR, po.ORDER_AVX2):
+        got = po.moe_layer(D, E, K, H, po.DT_BF16, 0, router, experts, stride, xb, order=order, bias=bias)
+        assert np.array_equal(got["routing"], want_routes)
+        assert np.allclose(got["weights"], want_w, rtol=1e-5, atol=1e-7)
+        f64, f64_routes = _f64_moe(router, experts, stride, D, E, K, H, po.DT_BF16, 0, xb, bias=bias)
+        assert np.array_equal(f64_routes, want_routes)
+        assert np.max(np.abs(got["moe"] - f64)) <= 1e-5 * max(1.0, np.max(np.abs(f64)))
