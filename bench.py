@@ -125,6 +125,9 @@ def main():
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="N",
                     help="only run N eager 512-token calls of layer 0 (uniform, then skewed routing) for kernel "
                          "traces and exit")
+    ap.add_argument("--profile-layout", choices=("blobs", "tiled"), default="blobs",
+                    help="with --profile-prefill: experts read in the .rbt2 storage format (default) or through the "
+                         "opt-in tiled copy")
     ap.add_argument("--profile-batch", type=int, default=0, metavar="B",
                     help="with --profile-forward: B sequences per step at the batched leg's context length")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -143,7 +146,7 @@ def main():
         profile_forward(args.profile_forward, args.profile_batch)
         return
     if args.profile_prefill > 0:
-        profile_prefill(args.profile_prefill)
+        profile_prefill(args.profile_prefill, args.profile_layout == "tiled")
         return
     if args.profile_decode > 0:
         profile_decode(args.profile_decode)
@@ -569,10 +572,11 @@ def profile_decode(steps):
     dev.close()
 
 
-def profile_prefill(calls):
+def profile_prefill(calls, tiled=False):
     """`calls` eager calls of the prefill leg's workload (512 tokens through layer 0 of the decode
     stack, same weights and inputs), uniform and then skewed routing, for kernel traces (no HIP
-    graphs, no bench line). Only layer 0's router and experts are filled."""
+    graphs, no bench line). Only layer 0's router and experts are filled. tiled: the grouped GEMMs
+    read the opt-in tiled copy of the experts, else the .rbt2 blobs."""
     from rabbitm2_amd import hip as rh
     dev = rh.Device(0)
     esz = 2
@@ -593,7 +597,8 @@ def profile_prefill(calls):
     moe = dev.malloc(T * D * 4)
     bias_dev = dev.upload_array(np.array([2.0] * 8 + [0.0] * (E - 8), np.float32))
     dev.set_router_order(rh.ORDER_AVX2)
-    dev.prefill_layout(rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride))
+    if tiled:
+        dev.prefill_layout(rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride))
     t0 = time.perf_counter()
     for bias in (None, bias_dev):
         L = rh.moe_layer_desc(D, E, K, H, rh.DT_BF16, 1, routers, experts, stride, bias)
@@ -601,8 +606,8 @@ def profile_prefill(calls):
         for _ in range(calls):
             dev.moe_dev(L, xb, T, moe=moe)
         dev.synchronize()
-    print(f"profile-prefill: {calls} eager 512-token calls each with uniform and skewed routing in "
-          f"{time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
+    print(f"profile-prefill: {calls} eager 512-token calls each with uniform and skewed routing "
+          f"({'tiled copy' if tiled else 'blobs'}) in {time.perf_counter() - t0:.3f} s", file=sys.stderr, flush=True)
     dev.close()
 
 

@@ -319,10 +319,11 @@ struct GTile {
 // STAGES * SBYTES bytes at LDS offset ring0.
 // Tile slot tau -> (expert e, column tile jt, row tile il of e's list), with m_off the prefix of the
 // experts' row tiles and nt column tiles. Expert-major (colmajor 0): e's tiles are consecutive, so an
-// expert's column tiles share its activation rows in one XCD's L2. Column-major (1): tau = jt * M + rt
-// over the M row tiles of all experts, so each XCD's contiguous share of the slots spans every
-// expert's row tiles for a few column tiles and a few long lists load all XCDs alike. Either way an
-// expert's row tiles of one column tile (one weight tile) are consecutive, on one XCD.
+// expert's column tiles share its activation rows in one XCD's L2. Column-major (1): tau = jc * M + rt
+// over the M row tiles of all experts (expert e's column tile (jc + e) mod nt), so each XCD's
+// contiguous share of the slots spans every expert's row tiles for a few column tiles and a few long
+// lists load all XCDs alike. Either way an expert's row tiles of one column tile (one weight tile) are
+// consecutive, on one XCD.
 __device__ __forceinline__ void tile_of(int tau, const int32_t *__restrict__ m_off, int E, int nt, int colmajor,
                                         int *e_out, int *jt_out, int *il_out) {
     const int M = m_off[E];
@@ -337,7 +338,10 @@ __device__ __forceinline__ void tile_of(int tau, const int32_t *__restrict__ m_o
     }
     const int e = lo;
     if (colmajor) {
-        *jt_out = jc;
+        // diagonal: slot column jc holds column tile (jc + e) mod nt of expert e, so the tiles that run
+        // together on one XCD are not all the same column tile of many experts (the experts' blobs are
+        // a multiple of 4 MiB apart, so those would stream congruent address windows at the same time)
+        *jt_out = jc + e % nt < nt ? jc + e % nt : jc + e % nt - nt;
         *il_out = key - m_off[e];
     } else {
         const int me = m_off[e + 1] - m_off[e], local = key - m_off[e] * nt;
@@ -795,7 +799,29 @@ constexpr int kWdWaves = 8, kWdGroups = 4;
 constexpr bool gemm_wide_supported(int mats, int N, int Kd) {
     return N % (mats == 2 ? 256 : 512) == 0 && Kd % (2 * kWrKC) == 0;
 }
-template <int MATS>
+
+// Weight operands straight from the row-major blobs. The matrix-core operand order (lane -> row
+// lane & 15, 16 bytes at 16 * (lane >> 4) of a 64-byte half-line) makes every load instruction touch
+// 16 rows x 64 B, which HBM serves at ~5.6 TB/s in this kernel's access pattern, against ~6.9 TB/s
+// when each instruction reads whole 128-byte lines (8 rows x 128 B; measured with read-only probes of
+// the same pattern). So each 16-row column group is loaded as two such instructions -- a: rows 0-7,
+// b: rows 8-15 of the group, lane -> row (lane & 7), 16-byte chunk 4 * bit3(lane) + (lane >> 4) of the
+// row's 128-byte k-step -- and turned into the operands by one row shift of 8 lanes each way:
+// afterwards a holds chunks 0-3 (k 0..31) and b chunks 4-7 (k 32..63) of row (lane & 15), the
+// operands of the step's two 32-wide halves in the usual order.
+__device__ __forceinline__ void blob_operands(u32x4 &a, u32x4 &b) {
+    u32x4 lo, hi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // lanes 8..15 of each 16-lane row take b from 8 lanes below; lanes 0..7 of hi take a from 8 above
+        lo[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)a[i], (int)b[i], 0x118, 0xF, 0xC, false);  // row_shr:8
+        hi[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)b[i], (int)a[i], 0x108, 0xF, 0x3, false);  // row_shl:8
+    }
+    a = lo;
+    b = hi;
+}
+
+template <int MATS, bool BLOB>
 __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
     const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
@@ -831,8 +857,12 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
     const size_t rowb = (size_t)Kd * 2;  // bytes per weight / activation-plane row
     const int nch = Kd / kWrKC;
     // step c reads k-chunk (c + rot) mod nch, rot a function of the weight tile and the same for the
-    // whole block (every wave stages the step's activation chunk for all of them)
-    const int rot = (e * ntiles_n + jt) % nch;
+    // whole block (every wave stages the step's activation chunk for all of them). Consecutive experts
+    // take consecutive rotations and column tiles nch / ntiles_n apart, so the weight tiles that run
+    // together on one XCD (a few experts' column tiles, or one column tile of many experts) start at
+    // different k-chunks: their row-major lines then spread over the L2 sets and DRAM channels that a
+    // k-window maps to (e * ntiles_n + jt left every expert of a column tile on nch / ntiles_n values).
+    const int rot = (e + jt * max(1, nch / ntiles_n)) % nch;
     auto cidx = [&](int c) { return c + rot < nch ? c + rot : c + rot - nch; };
     const int jn = 2 * jt + (MATS == 2 ? ((W & 3) >> 1) : (W >> 2));  // the 256-row tile of this wave's rows
 
@@ -840,7 +870,7 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
     // 8 * (lane >> 4) in each 32-wide half s of a 64-wide k-chunk cc, at wp + g * wg + cc * wck + s * wsb
     const uint8_t *wp;
     size_t wck, wsb, wg;
-    if (tiled) {
+    if constexpr (!BLOB) {
         // row block of the 256-row tile jn (tiled copy order, see prefill_layout_kernel)
         const int wn = MATS == 2 ? (W >= 4 ? 8 : 0) + 4 * (W & 1) : 4 * (W & 3);
         wp = tiled + (size_t)e * tiled_stride + tiled_off + (size_t)jn * nch * kTiledChunk + (size_t)(2 * wn) * 1024 +
@@ -849,11 +879,12 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
         wsb = 1024;
         wg = 2048;
     } else {
+        // whole 128-byte lines per load (blob_operands): slot s2 of group g holds rows 8 s2 .. 8 s2 + 7
         const uint8_t *base = experts + (size_t)e * stride + (MATS == 2 && W >= 4 ? w3_off : w_off);
-        const int wr = n0 + (MATS == 2 ? 64 * (W & 3) : 64 * W) + (lane & 15);
-        wp = base + (size_t)wr * rowb + 16 * (lane >> 4);
+        const int wr = n0 + (MATS == 2 ? 64 * (W & 3) : 64 * W) + (lane & 7);
+        wp = base + (size_t)wr * rowb + 16 * (4 * ((lane >> 3) & 1) + (lane >> 4));
         wck = ROWB;
-        wsb = 64;
+        wsb = 8 * rowb;
         wg = 16 * rowb;
     }
     const size_t base_row = gather ? 0 : (size_t)row0;
@@ -906,6 +937,10 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
         if constexpr (!LAST) load_a(aset[J], c + 2);
         if constexpr (!LAST || J == 0) load_w(wv[J ^ 1], c + 1);
         const uint8_t *st = ring[c & 1];
+        if constexpr (BLOB) {
+#pragma unroll
+            for (int g = 0; g < kWdGroups; ++g) blob_operands(wv[J][g][0], wv[J][g][1]);
+        }
 #pragma unroll
         for (int q = 0; q < RG; ++q) {
             if (16 * q < rows) {  // wave-uniform: the row group holds list entries
@@ -1136,9 +1171,13 @@ hipError_t launch_gemm_wide(const Launch &L, const uint8_t *experts, uint64_t st
     const long long tiles = (long long)max_mtiles * (N / (MATS == 2 ? 256 : 512));  // >= the 128-row tiles
     const long long blocks = (tiles + 7) / 8 * 8;
     if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
-    return launch(L, grouped_gemm_wide_kernel<MATS>, dim3((unsigned)blocks), dim3(64 * kWdWaves), 0, experts, stride,
-                  w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off128, choice, E, out_f32,
-                  out_hi, out_lo, tiled, tiled_stride, tiled_off);
+    if (tiled)
+        return launch(L, grouped_gemm_wide_kernel<MATS, false>, dim3((unsigned)blocks), dim3(64 * kWdWaves), 0, experts,
+                      stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off128, choice, E,
+                      out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
+    return launch(L, grouped_gemm_wide_kernel<MATS, true>, dim3((unsigned)blocks), dim3(64 * kWdWaves), 0, experts,
+                  stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off128, choice, E,
+                  out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
 }
 
 }  // namespace
