@@ -368,13 +368,23 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
         r -= sg.rows[s];
         ++s;
     }
-    const size_t koff = (size_t)w * WS * 32 + 8 * (lane >> 4);
-    const uint8_t *wp = sg.W[s] + ((size_t)(r + (lane & 15)) * K + koff) * 2;
     u32x4 a[RT][WS];
+    if constexpr (WS % 2 == 0) {
+        // pairs of k-steps as whole 128-byte lines per load, shuffled into operands (blob_operands)
+        const uint8_t *wp = sg.W[s] + ((size_t)(r + (lane & 7)) * K + (size_t)w * WS * 32) * 2 + 16 * blob_chunk(lane);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int i = 0; i < WS; ++i) a[rt][i] = ld_stream_u4(wp + (size_t)rt * 16 * K * 2 + 64 * i);
+            for (int i = 0; i < WS; ++i)
+                a[rt][i] = ld_stream_u4(wp + (size_t)rt * 16 * K * 2 + (size_t)(i & 1) * 8 * K * 2 + 128 * (i >> 1));
+    } else {
+        const size_t koff = (size_t)w * WS * 32 + 8 * (lane >> 4);
+        const uint8_t *wp = sg.W[s] + ((size_t)(r + (lane & 15)) * K + koff) * 2;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int i = 0; i < WS; ++i) a[rt][i] = ld_stream_u4(wp + (size_t)rt * 16 * K * 2 + 64 * i);
+    }
     f32x4 acc[RT][TB];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -398,6 +408,14 @@ __global__ __launch_bounds__(1024) void dense_mfma_kernel(const uint16_t *__rest
         // every load out before the first MFMA (the scheduler would otherwise reuse registers and
         // serialise round trips)
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (WS % 2 == 0) {
+            if (tb0 == 0) {
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int i = 0; i < WS; i += 2) blob_operands(a[rt][i], a[rt][i + 1]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < WS; ++i) {
 #pragma unroll

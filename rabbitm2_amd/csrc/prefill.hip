@@ -565,7 +565,7 @@ __global__ __launch_bounds__(256) void prefill_layout_kernel(const uint8_t *__re
 }
 
 // The block's work on 128-row tile slot `bid`; smem: 2 * 2 * ABYTES bytes of LDS (the ring).
-template <int MATS>
+template <int MATS, bool BLOB>
 __device__ __forceinline__ void gemm_wr_tile(
     uint8_t *smem, unsigned bid, const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off,
     int N, int Kd, const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather,
@@ -604,18 +604,19 @@ __device__ __forceinline__ void gemm_wr_tile(
     // tile's contiguous 32 KiB chunks)
     const uint8_t *wp;
     size_t wck, wsb;
-    if (tiled) {
+    if constexpr (!BLOB) {
         wp = tiled + (size_t)e * tiled_stride + tiled_off + (size_t)jt * nch * kTiledChunk + (size_t)(2 * W) * 1024 +
              16 * lane;
         wck = kTiledChunk;
         wsb = 1024;
     } else {
-        const int tr = 16 * W + (lane & 15);
-        const uint8_t *base = experts + (size_t)e * stride + (MATS == 2 && tr >= 128 ? w3_off : w_off);
+        // whole 128-byte lines per load (blob_operands): slot s of the step holds rows 8 s .. 8 s + 7
+        const int tr = 16 * W + (lane & 7);
+        const uint8_t *base = experts + (size_t)e * stride + (MATS == 2 && W >= 8 ? w3_off : w_off);
         const int wr = MATS == 2 ? n0 + (tr & 127) : n0 + tr;
-        wp = base + (size_t)wr * rowb + 16 * (lane >> 4);
+        wp = base + (size_t)wr * rowb + 16 * blob_chunk(lane);
         wck = ROWB;
-        wsb = 64;
+        wsb = 8 * rowb;
     }
     // activation units of this thread: u = tid + NT i -> plane i (u / (ABYTES / 16)), row, granule. They
     // are buffer loads: a row past the end of the list gets an offset past the buffer's end, which returns
@@ -671,6 +672,7 @@ __device__ __forceinline__ void gemm_wr_tile(
         if constexpr (!LAST) load_a(aset[J], c + SLOTS);
         if constexpr (!LAST || J + kWrAhead < SLOTS) load_w(wv[(J + kWrAhead) % SLOTS], c + kWrAhead);
         const uint8_t *st = ring[c & 1];
+        if constexpr (BLOB) blob_operands(wv[J][0], wv[J][1]);
 #pragma unroll
         for (int q = 0; q < RG; ++q) {
             if (16 * q < rows) {  // wave-uniform: the row group holds list entries
@@ -765,7 +767,7 @@ __device__ __forceinline__ void gemm_wr_tile(
 // ring (the 64-row tiles').
 constexpr int kSelLds = GTile<64, 256>::kStages * GTile<64, 256>::kStageBytes;
 static_assert(kSelLds >= 2 * 2 * kWrRows * 2 * kWrKC && GTile<64, 256>::kWaves == kWrWaves, "shared launch shape");
-template <int MATS>
+template <int MATS, bool BLOB>
 __global__ __launch_bounds__(64 * kWrWaves, 1) void grouped_gemm_sel_kernel(
     const uint8_t *__restrict__ experts, uint64_t stride, uint64_t w_off, uint64_t w3_off, int N, int Kd,
     const uint16_t *__restrict__ a_hi, const uint16_t *__restrict__ a_lo, int gather, const int32_t *__restrict__ perm,
@@ -776,7 +778,7 @@ __global__ __launch_bounds__(64 * kWrWaves, 1) void grouped_gemm_sel_kernel(
     __shared__ __align__(1024) uint8_t smem[kSelLds];
     const int plan = __builtin_amdgcn_readfirstlane(*choice), colmajor = plan >> 1;
     if (plan & 1)
-        gemm_wr_tile<MATS>(smem, blockIdx.x, experts, stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk,
+        gemm_wr_tile<MATS, BLOB>(smem, blockIdx.x, experts, stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk,
                            counts, offsets, m_off128, E, colmajor, out_f32, out_hi, out_lo, tiled, tiled_stride,
                            tiled_off);
     else
@@ -798,27 +800,6 @@ __global__ __launch_bounds__(64 * kWrWaves, 1) void grouped_gemm_sel_kernel(
 constexpr int kWdWaves = 8, kWdGroups = 4;
 constexpr bool gemm_wide_supported(int mats, int N, int Kd) {
     return N % (mats == 2 ? 256 : 512) == 0 && Kd % (2 * kWrKC) == 0;
-}
-
-// Weight operands straight from the row-major blobs. The matrix-core operand order (lane -> row
-// lane & 15, 16 bytes at 16 * (lane >> 4) of a 64-byte half-line) makes every load instruction touch
-// 16 rows x 64 B, which HBM serves at ~5.6 TB/s in this kernel's access pattern, against ~6.9 TB/s
-// when each instruction reads whole 128-byte lines (8 rows x 128 B; measured with read-only probes of
-// the same pattern). So each 16-row column group is loaded as two such instructions -- a: rows 0-7,
-// b: rows 8-15 of the group, lane -> row (lane & 7), 16-byte chunk 4 * bit3(lane) + (lane >> 4) of the
-// row's 128-byte k-step -- and turned into the operands by one row shift of 8 lanes each way:
-// afterwards a holds chunks 0-3 (k 0..31) and b chunks 4-7 (k 32..63) of row (lane & 15), the
-// operands of the step's two 32-wide halves in the usual order.
-__device__ __forceinline__ void blob_operands(u32x4 &a, u32x4 &b) {
-    u32x4 lo, hi;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // lanes 8..15 of each 16-lane row take b from 8 lanes below; lanes 0..7 of hi take a from 8 above
-        lo[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)a[i], (int)b[i], 0x118, 0xF, 0xC, false);  // row_shr:8
-        hi[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)b[i], (int)a[i], 0x108, 0xF, 0x3, false);  // row_shl:8
-    }
-    a = lo;
-    b = hi;
 }
 
 template <int MATS, bool BLOB>
@@ -882,7 +863,7 @@ __global__ __launch_bounds__(64 * kWdWaves, 1) void grouped_gemm_wide_kernel(
         // whole 128-byte lines per load (blob_operands): slot s2 of group g holds rows 8 s2 .. 8 s2 + 7
         const uint8_t *base = experts + (size_t)e * stride + (MATS == 2 && W >= 4 ? w3_off : w_off);
         const int wr = n0 + (MATS == 2 ? 64 * (W & 3) : 64 * W) + (lane & 7);
-        wp = base + (size_t)wr * rowb + 16 * (4 * ((lane >> 3) & 1) + (lane >> 4));
+        wp = base + (size_t)wr * rowb + 16 * blob_chunk(lane);
         wck = ROWB;
         wsb = 8 * rowb;
         wg = 16 * rowb;
@@ -1156,9 +1137,13 @@ hipError_t launch_gemm_sel(const Launch &L, const uint8_t *experts, uint64_t str
     const long long tiles = (long long)max_mtiles64 * (N / NTILE);  // >= the 128-row tiles
     const long long blocks = (tiles + 7) / 8 * 8;
     if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
-    return launch(L, grouped_gemm_sel_kernel<MATS>, dim3((unsigned)blocks), dim3(64 * kWrWaves), 0, experts, stride,
-                  w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, m_off128, choice, E,
-                  out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
+    if (tiled)
+        return launch(L, grouped_gemm_sel_kernel<MATS, false>, dim3((unsigned)blocks), dim3(64 * kWrWaves), 0, experts,
+                      stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, m_off128,
+                      choice, E, out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
+    return launch(L, grouped_gemm_sel_kernel<MATS, true>, dim3((unsigned)blocks), dim3(64 * kWrWaves), 0, experts,
+                  stride, w_off, w3_off, N, Kd, a_hi, a_lo, gather, perm, topk, counts, offsets, m_off64, m_off128, choice,
+                  E, out_f32, out_hi, out_lo, tiled, tiled_stride, tiled_off);
 }
 
 template <int MATS>

@@ -46,6 +46,30 @@ __device__ __forceinline__ f32x4 ld_stream_f4(const void *p) {
 }
 __device__ __forceinline__ f32x4 ld_f4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
 
+// Matrix-core weight operands straight from row-major bf16 rows. The operand order of
+// v_mfma_f32_16x16x32_bf16 (lane -> row lane & 15, 16 bytes at 16 * (lane >> 4) of a 64-byte half-line)
+// makes every load instruction touch 16 rows x 64 B, which HBM serves at ~5.3-5.6 TB/s in the grouped
+// GEMMs' access pattern, against ~6.6-6.9 TB/s when each instruction reads whole 128-byte lines
+// (8 rows x 128 B; measured with read-only probes of the same pattern). So a 16-row group's 128-byte
+// k-window (two 32-wide k-steps) is loaded as two such instructions -- a: rows 0-7, b: rows 8-15 of the
+// group, lane -> row (lane & 7), 16-byte chunk blob_chunk(lane) of the window -- and turned into the
+// operands by one row shift of 8 lanes each way: afterwards a holds chunks 0-3 (k 0..31) and b chunks
+// 4-7 (k 32..63) of row (lane & 15), the operands of the two k-steps in the usual order.
+__device__ __forceinline__ int blob_chunk(int lane) { return 4 * ((lane >> 3) & 1) + (lane >> 4); }
+
+__device__ __forceinline__ void blob_operands(u32x4 &a, u32x4 &b) {
+    u32x4 lo, hi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // lanes 8..15 of each 16-lane row take b from 8 lanes below; lanes 0..7 of hi take a from 8 above
+        lo[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)a[i], (int)b[i], 0x118, 0xF, 0xC, false);  // row_shr:8
+        hi[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)b[i], (int)a[i], 0x108, 0xF, 0x3, false);  // row_shl:8
+    }
+    a = lo;
+    b = hi;
+}
+
+
 // Cross-lane moves through DPP (a VALU operand modifier, no LDS round trip). Within each row of 16
 // lanes: swap neighbours, swap pairs, mirror each half-row, mirror the row -- after four steps every
 // lane of a row holds the same row total (each step adds commutative partners, so all lanes of a
