@@ -295,7 +295,7 @@ def main():
     dev.close()
 
 
-PROFILE_MAX_STEPS = 255  # eager steps timed per kernel (the library keeps 4096 event pairs per kernel)
+PROFILE_MAX_STEPS = 255  # eager steps timed per kernel at most (the workload has 255 timed steps)
 
 
 def profile_positions(pos_first, pos_last):

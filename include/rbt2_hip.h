@@ -282,9 +282,11 @@ void *rbt_hip_stream(rbt_hip *h); /* the hipStream_t all of this handle's work r
  * next step would time as "attn_norm". rbt_hip_generate is never timed this way. Modes (on):
  *   0  off.
  *   1  each call waits for its own kernels and adds their durations (eager calls only).
- *   2  deferred: each launch takes a fresh event pair and nothing waits, so timed calls run back
- *      to back as in a decode loop; rbt_hip_profile_get waits for the stream and returns the
- *      durations of every launch since the mode was set (at most 4096 per name are timed).
+ *   2  deferred: each launch takes an event pair stamped by the launch itself and nothing waits for
+ *      it, so timed _dev calls run back to back as in a decode loop; the pairs are read (and reused)
+ *      when a synchronous call (rbt_hip_moe, rbt_hip_forward, rbt_hip_forward_batch) has waited for its
+ *      own work, when 4096 pairs of one name are out, and by rbt_hip_profile_get, which returns the
+ *      durations of every launch since the mode was set.
  * Setting a mode clears the counts; neither mode is for stream capture (HIP graphs do not time
  * events). rbt_hip_profile_get fails for an unknown name. */
 int rbt_hip_profile_enable(rbt_hip *h, int on);

@@ -58,10 +58,11 @@ const char *const kProfNames[kProfCount] = {"router", "topk", "gateup", "down_co
                                             "lm_head", "argmax"};
 
 // mode 1: one event pair per kernel kind, read after every call (each call waits for its work).
-// mode 2 (deferred): every launch takes a fresh pair from a per-kind pool and nothing waits, so the
-// timed calls run back to back as in a decode loop; rbt_hip_profile_get reads every pair taken since
-// the mode was set. (HIP graphs do not time events, so neither mode is meant for stream capture.)
-constexpr size_t kProfPoolMax = 4096;  // pairs per kind in mode 2
+// mode 2 (deferred): every launch takes the next pair of a per-kind pool and nothing waits, so the
+// timed calls run back to back as in a decode loop; the pairs taken are read (and the pool reused) when
+// a synchronous call has waited for its work anyway, by rbt_hip_profile_get, or when a kind has
+// kProfPoolMax pairs out. (HIP graphs do not time events, so neither mode is meant for stream capture.)
+constexpr size_t kProfPoolMax = 4096;  // pairs per kind in mode 2 before a wait
 struct Profile {
     int mode = 0;
     hipEvent_t ev[kProfCount][2] = {};
@@ -69,7 +70,7 @@ struct Profile {
     double total_ms[kProfCount] = {};
     uint64_t launches[kProfCount] = {};
     std::vector<hipEvent_t> pool[kProfCount];  // mode 2: pairs (2i, 2i + 1)
-    size_t next[kProfCount] = {};
+    size_t next[kProfCount] = {};              // mode 2: pairs taken and not yet read
 };
 
 // Decode state of the full forward pass (rbt_hip_state_init): one allocation carved into the KV cache
@@ -416,6 +417,8 @@ int pin_reserve(rbt_hip *h, uint64_t bytes) {
     return 1;
 }
 
+int prof_harvest(rbt_hip *h);
+
 // The launch context of kernel k: the handle stream, plus (when profiling) the event pair that
 // hipExtLaunchKernel stamps with that kernel's own start and end.
 Launch lc(rbt_hip *h, int k) {
@@ -426,7 +429,8 @@ Launch lc(rbt_hip *h, int k) {
         L.start = P.ev[k][0];
         L.stop = P.ev[k][1];
         P.used[k] = true;
-    } else if (P.mode == 2 && k >= 0 && P.next[k] < kProfPoolMax) {
+    } else if (P.mode == 2 && k >= 0) {
+        if (P.next[k] == kProfPoolMax && !prof_harvest(h)) return L;  // this launch goes untimed
         std::vector<hipEvent_t> &pool = P.pool[k];
         while (pool.size() < 2 * (P.next[k] + 1)) {
             hipEvent_t ev = nullptr;
@@ -441,6 +445,27 @@ Launch lc(rbt_hip *h, int k) {
 }
 
 Launch lc_timed(rbt_hip *h, int k) { return lc(h, k); }
+
+// Mode 2: waits for the stream and adds the durations of every pair taken since the last read, which
+// frees the pools for reuse.
+int prof_harvest(rbt_hip *h) {
+    Profile &P = h->prof;
+    if (P.mode != 2) return 1;
+    bool any = false;
+    for (int k = 0; k < kProfCount; k++) any = any || P.next[k] > 0;
+    if (!any) return 1;
+    HIP_OK(h, hipStreamSynchronize(h->stream));
+    for (int k = 0; k < kProfCount; k++) {
+        for (size_t i = 0; i < P.next[k]; i++) {
+            float ms = 0.0f;
+            HIP_OK(h, hipEventElapsedTime(&ms, P.pool[k][2 * i], P.pool[k][2 * i + 1]));
+            P.total_ms[k] += ms;
+        }
+        P.launches[k] += P.next[k];
+        P.next[k] = 0;
+    }
+    return 1;
+}
 
 // Mode 1: waits for the call's events and adds each bracketed kernel's duration.
 int prof_collect(rbt_hip *h) {
@@ -1311,7 +1336,7 @@ int rbt_hip_moe(rbt_hip *h, int layer, const float *xb, int T, float *x_inout, i
     if (x_inout) memcpy(x_inout, pn + x_off, nx * 4);
     if (routing_out) memcpy(routing_out, pn + r_off, nr * 4);
     h->cache_hits += nr;  // every selected expert was resident
-    return 1;
+    return prof_harvest(h);
 }
 
 int rbt_hip_matvec_dev(rbt_hip *h, float *out_dev, const void *W_dev, int dtype, const float *x_dev, int rows,
@@ -1480,19 +1505,7 @@ int rbt_hip_profile_get(rbt_hip *h, const char *kernel, double *total_ms, uint64
     if (!h || !kernel) return fail(h, "profile_get: NULL argument");
     for (int k = 0; k < kProfCount; k++) {
         if (strcmp(kernel, kProfNames[k]) != 0) continue;
-        if (h->prof.mode == 2) {  // every pair taken since the mode was set
-            if (!set_device(h)) return 0;
-            HIP_OK(h, hipStreamSynchronize(h->stream));
-            double tot = 0.0;
-            for (size_t i = 0; i < h->prof.next[k]; i++) {
-                float ms = 0.0f;
-                HIP_OK(h, hipEventElapsedTime(&ms, h->prof.pool[k][2 * i], h->prof.pool[k][2 * i + 1]));
-                tot += ms;
-            }
-            if (total_ms) *total_ms = tot;
-            if (launches) *launches = h->prof.next[k];
-            return 1;
-        }
+        if (h->prof.mode == 2 && (!set_device(h) || !prof_harvest(h))) return 0;
         if (total_ms) *total_ms = h->prof.total_ms[k];
         if (launches) *launches = h->prof.launches[k];
         return 1;
@@ -1636,7 +1649,7 @@ int rbt_hip_forward(rbt_hip *h, int token, int pos, float *logits, int32_t *rout
                                  h->stream));
     HIP_OK(h, hipStreamSynchronize(h->stream));
     h->cache_hits += (uint64_t)c.n_layers * c.top_k;
-    return 1;
+    return prof_harvest(h);
 }
 
 int rbt_hip_generate(rbt_hip *h, const int32_t *prompt, int n_prompt, int n_gen, int32_t eos, int32_t *out,
@@ -1813,7 +1826,7 @@ int rbt_hip_forward_batch(rbt_hip *h, const int32_t *tokens, const int32_t *pos,
                                  hipMemcpyDeviceToHost, h->stream));
     HIP_OK(h, hipStreamSynchronize(h->stream));
     h->cache_hits += (uint64_t)c.n_layers * B * c.top_k;
-    return 1;
+    return prof_harvest(h);
 }
 
 int rbt_hip_generate_batch(rbt_hip *h, const int32_t *prompts, int n_prompt, int n_gen, int32_t *out, double *ms_out) {

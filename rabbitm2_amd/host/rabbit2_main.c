@@ -57,11 +57,11 @@ static void usage(const char *p) {
             p, p, p);
 }
 
-/* "moe: bytes=... GB/s=... %peak=...": the MoE blocks the library timed on the device with its deferred
- * HIP events (profiling mode 2; the --dump pass's eager forward() steps, at most 4096 blocks: the
- * --gen loop replays HIP graphs, whose kernels HIP does not time), their bytes as the engine's block
- * reads them (router rows and top_k experts' w1/w3/w2 per token and layer), against MI355X's published
- * 8 TB/s HBM peak. Nothing is printed when no block was timed. */
+/* "moe: bytes=... GB/s=... %peak=...": the MoE blocks the library timed on the device (its deferred
+ * kernel timing, profiling mode 2, in the --dump pass's eager forward() steps; the --gen loop replays
+ * HIP graphs, whose kernels HIP does not time): their kernels' summed durations, their bytes as the
+ * engine's block reads them (router rows and top_k experts' w1/w3/w2 per token and layer), and that
+ * rate against MI355X's published 8 TB/s HBM peak. Nothing is printed when no block was timed. */
 static int print_moe_line(rbt_hip *h, const rbt_config *c) {
     static const char *const kern[4] = {"router", "topk", "gateup", "down_combine"};
     double ms = 0.0, t = 0.0;
@@ -103,7 +103,7 @@ static int run(const char *path, const rbt_config *c, uint64_t expert_stride, in
     if (!rbt_hip_set_router_order(h, order) || !rbt_hip_upload_file(h, path, NULL)) goto done;
     if (cache_budget && !rbt_hip_set_option(h, "routing_history", 1)) goto done;
     if (!rbt_hip_state_init(h, ctx)) goto done;
-    if (!rbt_hip_profile_enable(h, 2)) goto done; /* device times of the MoE blocks, for the moe line */
+    if (!rbt_hip_profile_enable(h, 2)) goto done; /* kernel times of the MoE blocks, for the moe line */
 
     logits = (float *)malloc(sizeof(float) * (size_t)c->vocab);
     routing = (int32_t *)calloc((size_t)c->n_layers * c->top_k, sizeof(int32_t));

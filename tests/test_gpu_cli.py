@@ -97,6 +97,12 @@ def test_cli_eos_ctx_and_expert_cache_line(tmp_path):
     stride = po.layout(cfg)["expert_stride"]
     assert stats["evictions"] == 0 and stats["bytes_read"] == stats["misses"] * stride
     assert stats["hits"] + stats["misses"] == (len(tokens) + len(full) - 1) * cfg.n_layers * cfg.top_k
+    # the moe line: the --dump pass's blocks (one per prompt token and layer; the --gen loop is not timed)
+    esz = 2 if cfg.dtype == po.DT_BF16 else 4
+    moe = re.findall(r"^moe: bytes=(\d+) GB/s=([\d.]+) %peak=([\d.]+)$", err, re.M)
+    assert len(moe) == 1 and float(moe[0][1]) > 0, err
+    assert int(moe[0][0]) == len(tokens) * cfg.n_layers * esz * (cfg.n_experts * cfg.dim +
+                                                                 3 * cfg.top_k * cfg.expert_hidden * cfg.dim)
     out, err = run(path, "--gen", 2, "--kernel", "hip", *tokens)
     assert "matvec kernel: hip-gfx950" in err and len(out.split()) == 2
 
@@ -253,3 +259,39 @@ def test_expert_read_beyond_4gib(tmp_path, binary):
     res = subprocess.run([exe, str(small), "--gen", "1", "--expert-cache-mib", "1"] + kernel + ["1"],
                          capture_output=True, text=True, timeout=120)
     assert res.returncode != 0 and "budget too small" in res.stderr, res.stderr
+
+
+TIMING_RE = re.compile(r"prompt: (\d+) tokens in [\d.]+s \(([\d.]+) tok/s\)(?: \| generated (\d+) in [\d.]+s \(([\d.]+) tok/s\))?")
+MOE_RE = re.compile(r"^moe: bytes=(\d+) GB/s=([\d.]+) %peak=([\d.]+)$", re.M)
+
+
+@pytest.mark.skipif(not os.path.exists(PATCHED), reason="patched reference engine not built (oracle/Makefile ref_hip)")
+@pytest.mark.parametrize("case,n_gen", [("tiny_olmoe_f32", 32), ("olmoe_layer_bf16", 12)])
+def test_engine_drop_in_timing(tmp_path, case, n_gen):
+    """The drop-in timed as the engine times itself (its stderr line, rabbit2.c:742-744): the reference
+    engine with --kernel hip (the MoE block through rbt_hip_moe, the rest on the CPU) against the same
+    engine on the CPU alone (--kernel auto) on the same prompt: identical ids, and the moe line the
+    patch adds after the timing line (bytes as the engine's block reads them, GB/s from the library's
+    device times). Prints both rates."""
+    spec, cfg, path = write_case(case, tmp_path)
+    fx = np.load(os.path.join(GOLDEN, case + ".npz"))
+    tokens = [str(int(t)) for t in fx["tokens"]]
+    n_gen = min(n_gen, cfg.max_seq - len(tokens))
+    runs = {}
+    for name, exe, kernel in (("hip", PATCHED, "hip"), ("cpu", po.REF_BIN, "auto")):
+        res = subprocess.run([exe, str(path), "--gen", str(n_gen), "--kernel", kernel] + tokens, capture_output=True,
+                             text=True, timeout=300)
+        assert res.returncode == 0, res.stderr
+        m = TIMING_RE.search(res.stderr)
+        assert m and int(m.group(1)) == len(tokens) and int(m.group(3)) == n_gen, res.stderr
+        runs[name] = (res.stdout.split(), float(m.group(2)), float(m.group(4)), res.stderr)
+    assert runs["hip"][0] == runs["cpu"][0]
+    moe = MOE_RE.findall(runs["hip"][3])
+    assert len(moe) == 1, runs["hip"][3]
+    blocks = (len(tokens) + n_gen - 1) * cfg.n_layers
+    esz = 2 if cfg.dtype == po.DT_BF16 else 4
+    assert int(moe[0][0]) == blocks * esz * (cfg.n_experts * cfg.dim + 3 * cfg.top_k * cfg.expert_hidden * cfg.dim)
+    assert float(moe[0][1]) > 0
+    print(f"{case}: prompt {len(tokens)} + {n_gen} generated | engine --kernel hip: prompt {runs['hip'][1]:.1f} tok/s, "
+          f"gen {runs['hip'][2]:.1f} tok/s, moe {moe[0][1]} GB/s ({moe[0][2]}% of peak) | engine on the CPU: prompt "
+          f"{runs['cpu'][1]:.1f} tok/s, gen {runs['cpu'][2]:.1f} tok/s", flush=True)

@@ -156,6 +156,29 @@ def test_profile_deferred_mode(dev, olmoe_layer):
         dev.free(moe)
 
 
+def test_profile_deferred_mode_reuses_its_events(dev, olmoe_layer):
+    """Mode 2 reads its event pairs and reuses them: past 4096 launches of one kernel every launch is
+    still counted (the pool is read when it fills), and reading the counts between calls adds up."""
+    dev.set_router_order(po.ORDER_AVX2)
+    L = olmoe_layer.desc()
+    dev.reserve(L, 1)
+    xb = dev.upload_array(olmoe_layer.make_x(1, seed=9))
+    moe = dev.malloc(2048 * 4)
+    try:
+        dev.profile(2)
+        for _ in range(4100):
+            dev.moe_dev(L, xb, 1, moe=moe)
+        assert dev.profile_get("gateup")[1] == 4100
+        for _ in range(3):
+            dev.moe_dev(L, xb, 1, moe=moe)
+        tot, n = dev.profile_get("router")
+        assert n == 4103 and 0 < 1000.0 * tot / n < 1000.0
+    finally:
+        dev.profile(0)
+        dev.free(xb)
+        dev.free(moe)
+
+
 def test_olmoe_decode_deterministic(dev, olmoe_layer):
     dev.set_router_order(po.ORDER_AVX2)
     xb = olmoe_layer.make_x(1, seed=7)
