@@ -657,15 +657,23 @@ def read_model_image(dev, cfg):
 
 
 def cpu_full_model(dev, cfg, prompt, seconds):
-    """The engine's forward() (the oracle's orc_run, AVX2 order, bitwise the reference) on one host
-    core over a prefix of the prompt, on the same weights read back from HBM."""
+    """The CPU baseline of the headline: the reference engine itself (oracle/_ref/rabbit2, built from
+    rabbit2/src/rabbit2.c by oracle/Makefile) with its AVX2 matvec (--kernel avx2) on one host core, over
+    a prefix of the same prompt on the same weights (the device image written to a .rbt2 file in memory),
+    as its own stderr timing line reports it (rabbit2.c:742-744). Beside it, the oracle's forward() (the
+    C restatement, bitwise the same arithmetic) on the same prefix. Without the reference binary the
+    oracle's rate is the baseline (kind "port")."""
+    import re
+    import subprocess
+    import tempfile
     from oracle import pyoracle as po
     img = read_model_image(dev, cfg)
     try:
         old = os.sched_getaffinity(0)
-        os.sched_setaffinity(0, {sorted(old)[0]})
+        os.sched_setaffinity(0, {sorted(old)[0]})  # one core, inherited by the engine's process
     except (AttributeError, OSError):
         old = None
+    ref = None
     try:
         t0 = time.perf_counter()
         po.run(img, prompt[:1], order=po.ORDER_AVX2, ctx=len(prompt))
@@ -674,12 +682,29 @@ def cpu_full_model(dev, cfg, prompt, seconds):
         t0 = time.perf_counter()
         po.run(img, prompt[:n], order=po.ORDER_AVX2, ctx=len(prompt))
         dt = time.perf_counter() - t0
+        port = {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+                "sample": f"the oracle's forward() over the first {n} prompt tokens ({dt:.1f} s, one token per call "
+                          f"as the engine's loop); host {cpu_model()}"}
+        if po.have_ref():
+            shm = "/dev/shm" if os.path.isdir("/dev/shm") else None
+            with tempfile.TemporaryDirectory(dir=shm) as td:
+                path = os.path.join(td, "olmoe.rbt2")
+                img.tofile(path)
+                del img
+                cmd = [po.REF_BIN, path, "--dump", os.devnull, os.devnull, "--ctx", str(len(prompt)), "--kernel", "avx2"]
+                res = subprocess.run(cmd + [str(int(t)) for t in prompt[:n]], capture_output=True, text=True,
+                                     timeout=max(120.0, 10 * seconds))
+                m = re.search(r"prompt: (\d+) tokens in ([\d.]+)s \(([\d.]+) tok/s\)", res.stderr)
+                if res.returncode == 0 and m and "matvec kernel: avx2" in res.stderr:
+                    ref = {"value": float(m.group(3)), "unit": "tok/s", "cores": 1, "kind": "reference",
+                           "sample": f"the reference engine (oracle/_ref/rabbit2 --kernel avx2, built from "
+                                     f"rabbit2/src/rabbit2.c) over the first {m.group(1)} prompt tokens of the same "
+                                     f"prompt and weights, its own timing line ({m.group(2)} s); host {cpu_model()}",
+                           "port_cross_check": port}
     finally:
         if old is not None:
             os.sched_setaffinity(0, old)
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"forward() over the first {n} prompt tokens ({dt:.1f} s, one token per call as the engine's "
-                      f"loop); host {cpu_model()}"}
+    return ref if ref is not None else port
 
 
 
