@@ -16,7 +16,7 @@ The same JSON line carries:
             experts' w1/w3 rows, SwiGLU): algorithmic bytes / its average duration, from HIP events
             around every launch in eager forward() steps at the timed positions; traffic from the
             calibrated rocprofv3 counter runs kept under profiles/. --profile-forward 383 runs the same
-            eager steps for a kernel trace and prints the same event timings beside it.
+            eager steps for a kernel trace.
   layer     the MoE layer alone (the metric's "MoE-layer HBM GB/s & % of peak"): 16 OLMoE-shaped MoE
             layers with renormalised top-8, one token per step, each layer reading its own 100.9 MB,
             replayed from a HIP graph; per-layer time, HBM rate, per-kernel times; the host-pointer
@@ -268,8 +268,8 @@ def main():
             "timing": f"HIP events around each launch in eager forward() steps at {len(prof_pos)} of the timed "
                       f"positions ({prof_pos[0]}..{prof_pos[-1]}) x {cfg.n_layers} layers",
             "launches": dom["launches"],
-            "trace_check": "profiles/olmoe_forward_decode_kernels.md: rocprofv3 kernel trace and these HIP "
-                           "events of the same eager steps in one process (bench.py --profile-forward)",
+            "trace_check": "profiles/olmoe_forward_decode_kernels.md: these HIP event timings from a bench run "
+                           "beside a rocprofv3 kernel trace of the same eager steps (bench.py --profile-forward 383)",
         },
         "full_model": {
             "bytes_per_token": int(tok_bytes),
@@ -503,10 +503,10 @@ def make_full_model(dev):
 
 def profile_forward(steps, batch):
     """`steps` eager forward steps of the whole model over random ids, for kernel traces (no HIP graphs,
-    no bench line). batch 0: rbt_hip_forward at positions 0 .. steps-1, the positions from N_PROMPT on
-    also timed per kernel with HIP events as the bench times them (printed as one JSON line on stderr,
-    so a trace of this run and the bench's event timing can be compared launch for launch); 383 steps
-    are the bench's prompt and its 255 timed positions. batch B > 0: rbt_hip_forward_batch of B
+    no bench line). batch 0: rbt_hip_forward at positions 0 .. steps-1 (383 steps are the bench's prompt
+    and its 255 timed positions, the eager steps whose HIP event timings the bench reports; HIP events
+    taken under a profiler tool are not a check on its trace, the tool's instrumentation stretches
+    them). batch B > 0: rbt_hip_forward_batch of B
     sequences at positions B_CTX .. B_CTX + steps - 1 of the batched leg's context (the caches below
     hold the zeros of batch_init instead of a filled context; the kernels read the same bytes)."""
     from rabbitm2_amd import hip as rh
@@ -518,14 +518,8 @@ def profile_forward(steps, batch):
     if batch <= 0:
         dev.state_init(max(steps, 1))
         seq = rng.integers(0, cfg.vocab, steps).astype(np.int32).tolist()
-        n_pre = min(N_PROMPT, steps)
-        for p in range(n_pre):
+        for p in range(steps):
             dev.forward(seq[p], p, cfg.vocab, cfg.n_layers, cfg.top_k)
-        if steps > n_pre:
-            timed = list(range(n_pre, steps))
-            kern = eager_step_kernels(dev, cfg, seq, timed)
-            print(json.dumps({"profile_forward_events": kern, "positions": [timed[0], timed[-1]]}), file=sys.stderr,
-                  flush=True)
     else:
         dev.batch_init(batch, B_CTX + steps)
         for p in range(steps):
