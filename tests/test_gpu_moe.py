@@ -234,3 +234,74 @@ def test_router_batch_shapes(dev, shape):
             check(layer, xb, po.ORDER_AVX2, dev, label=f"router batch D{D}E{E}")
     finally:
         layer.close()
+
+
+# The engine's selection (rabbit2.c:516-528) scans with a strict '>' from index 0: among equal
+# probabilities the lowest index goes first, and when the softmax sum is NaN (every probability NaN)
+# each round keeps the first unused index. Every top-k on the GPU path is held to that exactly, with no
+# exemption for ties: the fused decode kernel (top-k inside gate/up), the separate top-k launch, the
+# few-token front end (top-k + activation split) and the one-launch grouped front end, in both orders.
+TOPK_PATHS = [  # (label, tokens, option fused_decode)
+    ("fused-decode", 1, 1), ("topk-launch", 1, 0), ("few-tokens", 5, 1), ("grouped-front", 16, 1),
+    ("grouped-one-launch", 100, 1)]
+
+
+def _selection_layer(dev, nan_row=None):
+    """D 512, 64 experts, top-8, H 512, bf16, renormalised. Router rows 7, 40 and 41 copy row 3 and rows
+    20 and 21 copy row 10, with biases +20 and +10 on the two groups: every token's eight largest
+    probabilities are a 4-way and a 3-way exact tie and one more expert. nan_row: that router row set to
+    bf16 NaN (0x7FC0), which makes the softmax sum and every probability NaN."""
+    bias = np.zeros(64, np.float32)
+    bias[[3, 7, 40, 41]] = 20.0
+    bias[[10, 20, 21]] = 10.0
+    layer = SynthLayer(dev, 512, 64, 8, 512, po.DT_BF16, 1, seed=21, bias=bias)
+    r = layer.router.copy()
+    r[[7, 40, 41]] = r[3]
+    r[[20, 21]] = r[10]
+    if nan_row is not None:
+        r[nan_row] = 0x7FC0
+    dev.h2d(layer.router_dev, r)
+    layer.router = r
+    return layer
+
+
+@pytest.mark.parametrize("order", ORDERS, ids=["avx2", "scalar"])
+@pytest.mark.parametrize("path", TOPK_PATHS, ids=[p[0] for p in TOPK_PATHS])
+def test_topk_exact_ties_take_the_lowest_index(dev, path, order):
+    label, T, fused = path
+    layer = _selection_layer(dev)
+    dev.set_router_order(order)
+    dev.set_option("fused_decode", fused)
+    try:
+        xb = layer.make_x(T, seed=70 + T)
+        want = layer.oracle(xb, order)
+        assert (want["routing"][:, :4] == [3, 7, 40, 41]).all() and (want["routing"][:, 4:7] == [10, 20, 21]).all()
+        probs = want["probs"].reshape(T, -1)
+        assert (probs[:, [7, 40, 41]] == probs[:, [3]]).all() and (probs[:, [20, 21]] == probs[:, [10]]).all()
+        got = layer.run_gpu(xb)
+        assert np.array_equal(got["routing"], want["routing"]), f"{label}: {got['routing'][0]} vs {want['routing'][0]}"
+        assert normwise_err(got["weights"], want["weights"]) <= 1e-6
+        assert normwise_err(got["moe"], want["moe"]) <= MOE_RTOL
+    finally:
+        dev.set_option("fused_decode", 1)
+        layer.close()
+
+
+@pytest.mark.parametrize("order", ORDERS, ids=["avx2", "scalar"])
+@pytest.mark.parametrize("path", TOPK_PATHS, ids=[p[0] for p in TOPK_PATHS])
+def test_topk_nan_probabilities_keep_the_first_indices(dev, path, order):
+    label, T, fused = path
+    layer = _selection_layer(dev, nan_row=33)
+    dev.set_router_order(order)
+    dev.set_option("fused_decode", fused)
+    try:
+        xb = layer.make_x(T, seed=90 + T)
+        want = layer.oracle(xb, order)
+        assert (want["routing"] == np.arange(8)).all() and np.isnan(want["weights"]).all()
+        got = layer.run_gpu(xb)
+        assert np.array_equal(got["routing"], want["routing"]), f"{label}: {got['routing'][0]}"
+        assert np.isnan(got["weights"]).all()
+        assert np.array_equal(np.isnan(got["moe"]), np.isnan(want["moe"]))
+    finally:
+        dev.set_option("fused_decode", 1)
+        layer.close()
