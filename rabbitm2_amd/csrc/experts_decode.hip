@@ -22,6 +22,7 @@ namespace {
 
 constexpr int KMAX_T = 64;  // selected experts per token (the engine's MAX_TOPK, rabbit2.c:59)
 constexpr int kDownThreads = 512, kDownRows = 1;  // down kernel: block size, output rows per wave
+constexpr int kDownPrefetch = 3;  // down kernel: weight slots in flight ahead of the dot products
 constexpr int kHStageMax = 8;  // 16-byte units of h per thread in the down kernel: K*H <= 16384 floats
 constexpr int EMAX_T = 64;  // experts per layer for the in-kernel top-k (one per lane of wave 0)
 
@@ -227,8 +228,9 @@ __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restr
 }
 
 // grid (ceil(D / (BT/64*RW)), T), block BT, dynamic LDS K*H*4 bytes; requires H == NH * 64 * kPer.
-// HS: 16-byte units of h staged per thread (K*H/4 <= BT*HS).
-template <int DT, int NH, int RW, int HS, int BT>
+// HS: 16-byte units of h staged per thread (K*H/4 <= BT*HS). PD: slots of weight rows in flight when
+// the block waits for h (0: every slot of the first chunk).
+template <int DT, int NH, int RW, int HS, int BT, int PD>
 __global__ __launch_bounds__(BT) void down_fast_kernel(const uint8_t *__restrict__ experts, uint64_t stride,
                                                         const int32_t *__restrict__ routing,
                                                         const float *__restrict__ weights,
@@ -249,9 +251,10 @@ __global__ __launch_bounds__(BT) void down_fast_kernel(const uint8_t *__restrict
     const int32_t *rt = routing + (size_t)t * K;
 
     // Load order: this thread's share of h first (small, from L2), then the weight loads of the first
-    // slot chunk, then the h stores to LDS. Loads complete in issue order, so the stores wait only for
-    // the h loads while every weight load is in flight, and the dot products below can start as
-    // soon as the first weights land instead of after the whole stream.
+    // PD slots, then the h stores to LDS. Loads complete in issue order, so the stores wait only for
+    // the h loads while those weight loads are in flight. After the barrier each slot's dot products
+    // run with the next PD slots in flight: a CU holds only so many outstanding misses, so a wave that
+    // issued its whole stream first would stall at its loads and compute only after the last one.
     const f32x4 *hsrc = reinterpret_cast<const f32x4 *>(hbuf + (size_t)t * K * H);
     f32x4 *hdst = reinterpret_cast<f32x4 *>(hs);
     const int units = K * H / 4;  // 16-byte units of h, at most HS per thread
@@ -261,22 +264,26 @@ __global__ __launch_bounds__(BT) void down_fast_kernel(const uint8_t *__restrict
     const float wsel = weights[(size_t)t * K + min(tid & 63, K - 1)];
 
     u32x4 w[KC][RW][NH];
-    auto load_chunk = [&](int k0, int nk) {
+    auto load_slot = [&](int k0, int nk, int kk) {
+        const int slot = k0 + (kk < nk ? kk : 0);  // clamped: always a valid expert row
+        const uint8_t *base = experts + (size_t)rt[slot] * stride + 2 * (size_t)H * D * kEsz;
 #pragma unroll
-        for (int kk = 0; kk < KC; ++kk) {
-            const int slot = k0 + (kk < nk ? kk : 0);  // clamped: always a valid expert row
-            const uint8_t *base = experts + (size_t)rt[slot] * stride + 2 * (size_t)H * D * kEsz;
+        for (int r = 0; r < RW; ++r) {
+            const int d = dbase + (r < nr ? r : 0);
 #pragma unroll
-            for (int r = 0; r < RW; ++r) {
-                const int d = dbase + (r < nr ? r : 0);
-#pragma unroll
-                for (int i = 0; i < NH; ++i)
-                    w[kk][r][i] = ld_stream_u4(base + ((size_t)d * H + (size_t)(lane + kWave * i) * kPer) * kEsz);
-            }
+            for (int i = 0; i < NH; ++i)
+                w[kk][r][i] = ld_stream_u4(base + ((size_t)d * H + (size_t)(lane + kWave * i) * kPer) * kEsz);
         }
     };
-    load_chunk(0, K < KC ? K : KC);
-    __builtin_amdgcn_sched_barrier(0);  // all weight loads issued before the h stores wait on h
+    auto load_chunk = [&](int k0, int nk) {
+#pragma unroll
+        for (int kk = 0; kk < KC; ++kk) load_slot(k0, nk, kk);
+    };
+    constexpr int P0 = PD > 0 && PD < KC ? PD : KC;
+    const int nk0 = K < KC ? K : KC;
+#pragma unroll
+    for (int kk = 0; kk < P0; ++kk) load_slot(0, nk0, kk);
+    __builtin_amdgcn_sched_barrier(0);  // these weight loads issued before the h stores wait on h
     // unconditional stores (clamped lanes rewrite the last unit with the same data): a store behind a
     // branch would let the compiler sink its load into the branch, after the weight stream
 #pragma unroll
@@ -291,35 +298,42 @@ __global__ __launch_bounds__(BT) void down_fast_kernel(const uint8_t *__restrict
     float moe[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) moe[r] = 0.0f;
+    // slot kk's products: its rows . h_kk over the lane's elements, then the wave sum
+    auto slot_dot = [&](int k0, int nk, int kk, float (&acc)[RW]) {
+        const float *hk = hs + (size_t)(k0 + (kk < nk ? kk : 0)) * H;
+#pragma unroll
+        for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NH; ++i) {
+            const float *hp = hk + (lane + kWave * i) * kPer;
+#pragma unroll
+            for (int r = 0; r < RW; ++r) acc[r] += dot16<DT>(w[kk][r][i], hp);
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) acc[r] = wave_sum(acc[r]);
+    };
+    auto add_slot = [&](int k0, int kk, const float (&acc)[RW]) {
+        const float wk = s_w[k0 + kk];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+#pragma clang fp contract(off)
+            moe[r] = moe[r] + wk * acc[r];  // rabbit2.c:540, rounded product then add
+        }
+    };
+#pragma unroll
+    for (int kk = 0; kk < KC; ++kk) {
+        if (kk + P0 < KC) load_slot(0, nk0, kk + P0);  // P0 slots ahead of the one computed now
+        __builtin_amdgcn_sched_barrier(0);
+        float acc[RW];
+        slot_dot(0, nk0, kk, acc);
+        if (kk < nk0) add_slot(0, kk, acc);
+    }
     auto process = [&](int k0, int nk) {
         float acc[KC][RW];
 #pragma unroll
-        for (int kk = 0; kk < KC; ++kk) {
-            const float *hk = hs + (size_t)(k0 + (kk < nk ? kk : 0)) * H;
-#pragma unroll
-            for (int r = 0; r < RW; ++r) acc[kk][r] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NH; ++i) {
-                const float *hp = hk + (lane + kWave * i) * kPer;
-#pragma unroll
-                for (int r = 0; r < RW; ++r) acc[kk][r] += dot16<DT>(w[kk][r][i], hp);
-            }
-        }
-#pragma unroll
-        for (int kk = 0; kk < KC; ++kk) {
-#pragma unroll
-            for (int r = 0; r < RW; ++r) acc[kk][r] = wave_sum(acc[kk][r]);
-        }
-        for (int kk = 0; kk < nk; ++kk) {
-            const float wk = s_w[k0 + kk];
-#pragma unroll
-            for (int r = 0; r < RW; ++r) {
-#pragma clang fp contract(off)
-                moe[r] = moe[r] + wk * acc[kk][r];  // rabbit2.c:540, rounded product then add
-            }
-        }
+        for (int kk = 0; kk < KC; ++kk) slot_dot(k0, nk, kk, acc[kk]);
+        for (int kk = 0; kk < nk; ++kk) add_slot(k0, kk, acc[kk]);
     };
-    process(0, K < KC ? K : KC);
     for (int k0 = KC; k0 < K; k0 += KC) {
         const int nk = K - k0 < KC ? K - k0 : KC;
         load_chunk(k0, nk);
@@ -362,12 +376,12 @@ hipError_t down_nh(const Launch &L, const uint8_t *E, uint64_t stride, const int
     const uint32_t lds = (uint32_t)((size_t)K * H * 4);
     const int per = (K * H / 4 + BT - 1) / BT;  // h units per thread
     if (per <= 2)
-        return launch(L, down_fast_kernel<DT, NH, RW, 2, BT>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
+        return launch(L, down_fast_kernel<DT, NH, RW, 2, BT, kDownPrefetch>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
                       x_inout, moe_out);
     if (per <= 4)
-        return launch(L, down_fast_kernel<DT, NH, RW, 4, BT>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
+        return launch(L, down_fast_kernel<DT, NH, RW, 4, BT, kDownPrefetch>, g, b, lds, E, stride, routing, weights, hbuf, K, D,
                       x_inout, moe_out);
-    return launch(L, down_fast_kernel<DT, NH, RW, kHStageMax, BT>, g, b, lds, E, stride, routing, weights, hbuf, K,
+    return launch(L, down_fast_kernel<DT, NH, RW, kHStageMax, BT, kDownPrefetch>, g, b, lds, E, stride, routing, weights, hbuf, K,
                   D, x_inout, moe_out);
 }
 
