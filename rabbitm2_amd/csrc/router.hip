@@ -189,12 +189,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 // rows of one token, thread (row rr, chain c). DR = 2 while the blocks fit the CUs once (each block
 // stages x plus fewer weight bytes before its chains start; one OLMoE MoE layer 24.4 against 24.7 us
 // with 4 rows), lanes 32-63 then staging only; DR = 4 for more tokens (at 32 tokens 5.5 against
-// 7.2 us: every block stages its token's x). Chain c's operands are staged transposed in LDS --
-// wt[rr][c][m] = W[r][16m + c], xt[c][m] = x[16m + c] -- so a 16-byte read carries 8 steps of one
-// chain (48 reads for 128 steps instead of 256 narrow ones) and the chain's dependent adds are the
-// only long pole. Staging: a thread takes 8 consecutive steps of 8 chains (eight 16-byte loads of
-// the row) and transposes them in registers (v_perm pairs the 16-bit halves) into eight 16-byte
-// LDS stores. The 16 chains of a row sit in 16 consecutive lanes: (chain j) + (chain 8+j) via a
+// 7.2 us: every block stages its token's x). Chain c's operands are staged transposed in LDS, both as
+// f32 -- wt[rr][c][m] = W[r][16m + c], xt[c][m] = x[16m + c] -- so two 16-byte reads of each carry 4
+// steps of one chain, and a step is one rounded multiply and one add (the bf16 weights are widened
+// once, while staging, not in the chain): the chain's dependent adds are the only long pole.
+// Staging: a thread takes 8 consecutive steps of 8 chains (eight 16-byte loads of the row), widens
+// and transposes them in registers into sixteen 16-byte LDS stores. The 16 chains of a row sit in
+// 16 consecutive lanes: (chain j) + (chain 8+j) via a
 // DPP row rotation, then the sequential sum over j, as the engine's lanes a[j] + b[j].
 // NORM: the kernel also runs the RMSNorm in front of the router (rabbit2.c:512): x is the residual
 // stream, xb = x * inv * nw with inv = 1/sqrtf(sum x^2 / D + eps) from the block's own staging loads,
@@ -205,12 +206,12 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
                                                           float *__restrict__ logits, const float *__restrict__ nw = nullptr,
                                                           float eps = 0.0f, float *__restrict__ xb_out = nullptr) {
     constexpr int D = 16 * M;
-    constexpr int WP = M + 8;  // bf16 per (row, chain) line: 16-byte pad, lanes of one read hit distinct banks
+    constexpr int WP = M + 4;  // f32 per (row, chain) line: 16-byte pad, lanes of one read hit distinct banks
     constexpr int XP = M + 4;  // f32 per chain line
     constexpr int G = M / 8;   // 8-step groups per chain
     constexpr int kDRows = DR;
     static_assert(DR == 2 || DR == 4, "rows per block");
-    __shared__ __align__(16) uint16_t wt[kDRows * 16 * WP];
+    __shared__ __align__(16) float wt[kDRows * 16 * WP];  // the weights widened to f32 (exact)
     __shared__ __align__(16) float xt[16 * XP];
     const int tid = threadIdx.x, rr = tid >> 4, c = tid & 15;
     const int t = blockIdx.y, r0 = blockIdx.x * kDRows;
@@ -296,15 +297,17 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
         const int row = task / (2 * G), h = (task / G) & 1, g = task % G;
 #pragma unroll
         for (int ch = 0; ch < 8; ++ch) {
-            // chain 8h+ch, steps 8g..8g+7: bf16 #ch of units i = 0..7; dword k packs units 2k, 2k+1
-            uint32_t d[4];
+            // chain 8h+ch, steps 8g..8g+7: bf16 #ch of units i = 0..7, widened here once by all lanes
+            // instead of in every step of the chain (ch odd: the high halves)
+            uint32_t d[8];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t a = wv[q][2 * k][ch >> 1], b = wv[q][2 * k + 1][ch >> 1];
-                // low half = unit 2k's bf16, high half = unit 2k+1's; ch odd selects the high halves
-                d[k] = (ch & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t u = wv[q][i][ch >> 1];
+                d[i] = (ch & 1) ? (u & 0xFFFF0000u) : (u << 16);
             }
-            *reinterpret_cast<u32x4 *>(&wt[(row * 16 + 8 * h + ch) * WP + 8 * g]) = u32x4{d[0], d[1], d[2], d[3]};
+            float *dst = &wt[(row * 16 + 8 * h + ch) * WP + 8 * g];
+            *reinterpret_cast<u32x4 *>(dst) = u32x4{d[0], d[1], d[2], d[3]};
+            *reinterpret_cast<u32x4 *>(dst + 4) = u32x4{d[4], d[5], d[6], d[7]};
         }
     }
 #pragma unroll
@@ -326,22 +329,23 @@ __global__ __launch_bounds__(64) void router_decode_kernel(const float *__restri
     __syncthreads();
 
     // ---- chain c of row rr, 128 steps in column order (rounded product, then add)
-    const uint16_t *wl = &wt[(min(rr, kDRows - 1) * 16 + c) * WP];  // lanes past the rows: clamped, no write
+    const float *wl = &wt[(min(rr, kDRows - 1) * 16 + c) * WP];  // lanes past the rows: clamped, no write
     const float *xl = &xt[c * XP];
     float acc = 0.0f;
 #pragma unroll 4
     for (int g = 0; g < G; ++g) {
-        const u32x4 w8 = *reinterpret_cast<const u32x4 *>(wl + 8 * g);
+        const f32x4 wa = *reinterpret_cast<const f32x4 *>(wl + 8 * g);
+        const f32x4 wc = *reinterpret_cast<const f32x4 *>(wl + 8 * g + 4);
         const f32x4 xa = *reinterpret_cast<const f32x4 *>(xl + 8 * g);
         const f32x4 xc = *reinterpret_cast<const f32x4 *>(xl + 8 * g + 4);
-        acc = acc + bf16_lo(w8.x) * xa.x;
-        acc = acc + bf16_hi(w8.x) * xa.y;
-        acc = acc + bf16_lo(w8.y) * xa.z;
-        acc = acc + bf16_hi(w8.y) * xa.w;
-        acc = acc + bf16_lo(w8.z) * xc.x;
-        acc = acc + bf16_hi(w8.z) * xc.y;
-        acc = acc + bf16_lo(w8.w) * xc.z;
-        acc = acc + bf16_hi(w8.w) * xc.w;
+        acc = acc + wa.x * xa.x;
+        acc = acc + wa.y * xa.y;
+        acc = acc + wa.z * xa.z;
+        acc = acc + wa.w * xa.w;
+        acc = acc + wc.x * xc.x;
+        acc = acc + wc.y * xc.y;
+        acc = acc + wc.z * xc.z;
+        acc = acc + wc.w * xc.w;
     }
     // lanes c and c+8 of the row: row_ror:8 brings chain c+8 to lane c
     const float other = __builtin_bit_cast(
