@@ -27,18 +27,20 @@ constexpr int kHStageMax = 8;  // 16-byte units of h per thread in the down kern
 constexpr int EMAX_T = 64;  // experts per layer for the in-kernel top-k (one per lane of wave 0)
 
 // Softmax + top-k of one token's logits, the engine's arithmetic (rabbit2.c:399-405, :516-528,
-// :539): leaves the expert ids in s_idx[0..K) and the combine weights in s_w[0..K). Called by every
-// thread of the block (it ends with a barrier); wave 0 does the work, exchanging values through
-// LDS with wave-scope fences only (a wave's LDS operations execute in order).
+// :539): leaves the expert ids in s_idx[0..nr) (the first nr <= K places; a round's place does not
+// depend on the later rounds) and, with all_k, every place and the combine weights in s_w[0..K).
+// Called by every thread of the block (it ends with a barrier); wave 0 does the work, exchanging
+// values through LDS with wave-scope fences only (a wave's LDS operations execute in order).
 __device__ __forceinline__ void wave_lds_sync() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 // XS > 0: the block also stages the token's activation row x (xu 16-byte units, at most XS per
 // thread, clamped loads and stores) into xs_lds; its loads are issued next to the logits load, so
 // they land while wave 0 selects.
 template <int XS = 0>
-__device__ __forceinline__ void block_topk(const float *__restrict__ logits, int E, int K, int norm_topk, float *s_v, int *s_idx,
-                           float *s_pw, float *s_w, const float *__restrict__ x = nullptr, f32x4 *xs_lds = nullptr,
-                           int xu = 0) {
+__device__ __forceinline__ void block_topk(const float *__restrict__ logits, int E, int K, int nr, bool all_k,
+                                           int norm_topk, float *s_v, int *s_idx, float *s_pw, float *s_w,
+                                           const float *__restrict__ x = nullptr, f32x4 *xs_lds = nullptr,
+                                           int xu = 0) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     f32x4 xv[XS > 0 ? XS : 1];
     if constexpr (XS > 0) {
@@ -91,25 +93,28 @@ __device__ __forceinline__ void block_topk(const float *__restrict__ logits, int
                     cand = -2.0f;
                 }
             };
-            if (K == 8) {  // the common top-8, unrolled
+            const int n = all_k ? K : nr;
+            if (n == 8) {  // the common top-8, unrolled
 #pragma unroll
                 for (int k = 0; k < 8; ++k) round(k);
             } else {
-                for (int k = 0; k < K; ++k) round(k);
+                for (int k = 0; k < n; ++k) round(k);
             }
         }
         wave_lds_sync();
-        float wsum = 0.0f;
-        if (K <= 8) {  // one LDS round trip instead of K dependent ones; the engine's order
-            const f32x4 a = reinterpret_cast<const f32x4 *>(s_pw)[0], b = reinterpret_cast<const f32x4 *>(s_pw)[1];
-            const float pw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        if (all_k) {  // the combine weights, for the block that publishes them
+            float wsum = 0.0f;
+            if (K <= 8) {  // one LDS round trip instead of K dependent ones; the engine's order
+                const f32x4 a = reinterpret_cast<const f32x4 *>(s_pw)[0], b = reinterpret_cast<const f32x4 *>(s_pw)[1];
+                const float pw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (k < K) wsum = wsum + pw[k];
-        } else {
-            for (int k = 0; k < K; ++k) wsum = wsum + s_pw[k];
+                for (int k = 0; k < 8; ++k)
+                    if (k < K) wsum = wsum + pw[k];
+            } else {
+                for (int k = 0; k < K; ++k) wsum = wsum + s_pw[k];
+            }
+            if (lane < K) s_w[lane] = norm_topk ? s_pw[lane] / wsum : s_pw[lane];
         }
-        if (lane < K) s_w[lane] = norm_topk ? s_pw[lane] / wsum : s_pw[lane];
     }
     __syncthreads();
 }
@@ -149,8 +154,9 @@ __device__ __forceinline__ float dot16r(const u32x4 w, const f32x4 x0, const f32
 
 // grid: ceil(P*H/JW / 4) blocks of 4 waves; requires H % JW == 0 and D == NC * 64 * kPer.
 // TOPK (batch 1 only): every block first runs the token's softmax + top-k from the router logits
-// (`logits`, E experts) instead of reading `routing`; block 0 publishes routing/weights for the
-// down kernel. Saves a launch on the decode critical path.
+// (`logits`, E experts) instead of reading `routing`, as far as the slots of its items; the last block
+// runs all K places and publishes routing/weights for the down kernel. Saves a launch on the decode
+// critical path.
 // With TOPK (one token) the block stages x in LDS once (XS units per thread) instead of every wave
 // reading all of it from L2.
 template <int DT, int NC, int JW, bool TOPK>
@@ -172,8 +178,13 @@ __global__ __launch_bounds__(256) void gateup_fast_kernel(const uint8_t *__restr
         __shared__ int s_idx[KMAX_T];
         __shared__ __align__(16) float s_pw[KMAX_T];
         __shared__ float s_w[KMAX_T];
-        block_topk<XS>(logits, E, K, norm_topk, s_v, s_idx, s_pw, s_w, xb, xs_lds, D / 4);
-        if (blockIdx.x == 0 && (int)threadIdx.x < K) {
+        // the block's items lie in slots 0 .. that of its last item, so it needs that many selection
+        // rounds; the last block holds slot K - 1 and publishes routing and weights for the down kernel
+        const long long last = min(items, (long long)(blockIdx.x + 1) * (blockDim.x / kWave)) - 1;
+        const int nr = (int)((last * JW) / H) + 1;
+        const bool pub = blockIdx.x == gridDim.x - 1;
+        block_topk<XS>(logits, E, K, nr, pub, norm_topk, s_v, s_idx, s_pw, s_w, xb, xs_lds, D / 4);
+        if (pub && (int)threadIdx.x < K) {
             routing[threadIdx.x] = s_idx[threadIdx.x];
             weights[threadIdx.x] = s_w[threadIdx.x];
         }
