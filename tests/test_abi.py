@@ -87,3 +87,14 @@ def test_bench_refuses_graph_replay_under_a_profiler():
                          text=True, timeout=120)
     assert res.returncode == 2
     assert "profiler" in res.stderr and "--profile-" in res.stderr
+
+
+@pytest.mark.parametrize("args,msg", [(["--gpus", "2"], "one GPU only"), (["--steps", "0"], "--steps must be")])
+def test_bench_refuses_what_it_does_not_measure(args, msg):
+    """More than one GPU (the sharded layer is a design note) and a non-positive step count end the bench
+    with a message before anything touches a device."""
+    env = {k: v for k, v in os.environ.items() if k not in PROFILER_VARS}
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py")] + args, env=env, capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode != 0
+    assert msg in res.stderr
